@@ -1,0 +1,323 @@
+"""Benchmark of the paged KV-cache decode path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-model] [--no-cpu]
+
+Workload (the configuration the metric is quoted on):
+bf16 MQA, 12 layers, batch 128 sequences, 16 query heads, 1 KV head,
+head_dim 64, context lengths U[256, 2048] (seed 0), block_size 16, a
+16384-block pool per layer, tables a random permutation of pool blocks.
+One STEP is the path's work for one decode step of that batch: for each of
+the 12 layers, the slot-mapped append of the 128 new K/V rows and the paged
+MQA decode attention over the layer's pool. K/V, Q and metadata are resident
+in HBM before timing starts.
+
+Printed JSON line:
+  value        algorithmic HBM bytes of the timed steps / their wall time
+               (GB/s), bytes as documented in DESIGN.md (K/V rows read,
+               Q read, O written, block-table entries used, append rows);
+  decode_tok_s full model decode step (dense layers in torch + this path,
+               greedy argmax on device) at batch 128, tokens/s;
+  roofline     the attention kernel alone: bytes per launch / mean launch
+               time from HIP events on its stream, against 8 TB/s;
+  north_star   the same kernel on config 5 (Hq 32, D 128, batch 256,
+               lognormal context mean 1024, fragmented tables);
+  cpu_baseline the reference's PyTorch path (index_select gather + SDPA,
+               the oracle) on this host's cores, on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "tiny-transformer-inference-engine_amd")
+for _p in (PKG, REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged MQA decode HBM GB/s (% of peak); decode tok/s at batch 128"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def attn_bytes(lens, hq, hkv, d, esize, bs):
+    """Algorithmic bytes of one decode attention launch (same formula as the
+    oracle's decode_attention_bytes, restated so the product bench does not
+    depend on the oracle): K+V rows of every visible token, Q in, O out,
+    4 B per block-table entry used, 4 B per seq_len."""
+    kv = int(sum(int(x) for x in lens))
+    n = len(lens)
+    blocks = sum((int(x) + bs - 1) // bs for x in lens)
+    return kv * hkv * d * 2 * esize + 2 * n * hq * d * esize + 4 * blocks + 4 * n
+
+
+def append_bytes(n_tok, hkv, d, esize, n_seq):
+    """K and V rows read and written, plus the int32 metadata the kernel reads
+    (table entry, query_start_loc, start_pos per token, amortised)."""
+    return 4 * n_tok * hkv * d * esize + 4 * (n_tok + 2 * n_seq + 1)
+
+
+def time_events(fn, iters, stream):
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters * 1e-3  # seconds per call
+
+
+def cfg4_tables(lens, bs, num_blocks, extra_tokens, seed):
+    from serving import workloads
+    return workloads.permuted_tables([int(x) + extra_tokens for x in lens], bs, num_blocks, seed)
+
+
+def run_hot_path(args, torch):
+    """Config-4 hot path: 12 x (append + paged decode attention)."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_attention_meta
+    from serving.kv_pool import KVPool
+    from serving.paged_meta import pack_batch_meta
+
+    dev = torch.device("cuda:0")
+    L, N, HQ, HKV, D, BS, NB = 12, 128, 16, 1, 64, 16, 16384
+    lens = workloads.lengths_uniform(N, 256, 2048, seed=0)
+    tables = cfg4_tables(lens, BS, NB, 1, seed=0)
+    pool = KVPool(L, BS, NB, HKV, D, torch.bfloat16, dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    for l in range(L):
+        pool.kv[l].normal_(generator=g)
+    # the step appends each sequence's token at position lens[i] and attends
+    # over lens[i] + 1 keys
+    pos = [int(x) for x in lens]
+    meta = pack_batch_meta(tables, list(range(N + 1)), pos, N, dev, BS)
+    q = torch.randn(N, HQ, D, generator=g, device=dev).bfloat16()
+    knew = torch.randn(N, HKV, D, generator=g, device=dev).bfloat16()
+    vnew = torch.randn(N, HKV, D, generator=g, device=dev).bfloat16()
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        for l in range(L):
+            pool.write_from_table(l, knew, vnew, meta)
+            paged_attention_meta(q, pool.kv[l, 0], pool.kv[l, 1], meta, out=out)
+
+    kv_after = lens + 1
+    per_layer_attn = attn_bytes(kv_after, HQ, HKV, D, 2, BS)
+    per_layer_app = append_bytes(N, HKV, D, 2, N)
+    step_bytes = L * (per_layer_attn + per_layer_app)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sec = time_events(step, args.steps, stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    log(f"hot path: {sec * 1e6:.1f} us/step (events), {wall * 1e6:.1f} us/step (wall)")
+
+    # the dominant kernel alone: attention on layer 0, back to back
+    def attn():
+        paged_attention_meta(q, pool.kv[0, 0], pool.kv[0, 1], meta, out=out)
+    for _ in range(5):
+        attn()
+    a_sec = time_events(attn, 200, stream)
+    log(f"attention alone: {a_sec * 1e6:.2f} us/launch, {per_layer_attn / 1e6:.2f} MB")
+    return dict(step_sec=sec, wall_sec=wall, step_bytes=step_bytes,
+                attn_sec=a_sec, attn_bytes=per_layer_attn, lens=lens, tables=tables,
+                pool=pool, q=q, meta=meta)
+
+
+def run_model(args, torch):
+    """Full bf16 model decode step at batch 128 (config 4), tokens/s."""
+    from serving import workloads
+    from serving.kv_pool import KVPool
+    from serving.layers import ModelConfig
+    from serving.paged_meta import pack_batch_meta
+    from serving.paged_model import PagedTransformer
+
+    dev = torch.device("cuda:0")
+    steps = args.model_steps
+    cfg = ModelConfig(vocab_size=50257, d_model=1024, num_layers=12, num_heads=16,
+                      num_kv_heads=1, max_seq_len=4096)
+    torch.manual_seed(0)
+    model = PagedTransformer(cfg).to(dev, torch.bfloat16).eval()
+    N, BS, NB = 128, 16, 16384
+    lens = workloads.lengths_uniform(N, 256, 2048, seed=0)
+    tables = cfg4_tables(lens, BS, NB, steps + args.warmup + 1, seed=0)
+    pool = KVPool(cfg.num_layers, BS, NB, 1, cfg.head_dim, torch.bfloat16, dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    for l in range(cfg.num_layers):
+        pool.kv[l].normal_(generator=g)
+    meta = pack_batch_meta(tables, list(range(N + 1)), [int(x) for x in lens], N, dev, BS)
+    ids = torch.randint(0, cfg.vocab_size, (N,), generator=g, device=dev)
+
+    def step():
+        nonlocal ids
+        logits = model.forward_step(ids, pool, meta)
+        ids = logits.argmax(-1)
+        # advance every sequence by one token, on the device
+        meta.positions.add_(1)
+        meta.start_pos.add_(1)
+        meta.seq_lens.add_(1)
+        meta.max_kv_len += 1
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        sec = time_events(step, steps, torch.cuda.current_stream(dev))
+    log(f"model decode step: {sec * 1e3:.3f} ms, {N / sec:.0f} tok/s")
+    return dict(step_sec=sec, tok_s=N / sec)
+
+
+def run_north_star(args, torch):
+    """Config 5 attention kernel alone (bs 16): achieved GB/s."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_mqa_decode
+
+    dev = torch.device("cuda:0")
+    p = workloads.cfg5_problem(dev, seed=0, bs=16)
+    out = torch.empty_like(p.q)
+    mk = int(p.lens.max())
+
+    def attn():
+        paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens,
+                         max_kv_len=mk, out=out)
+    for _ in range(5):
+        attn()
+    sec = time_events(attn, 100, torch.cuda.current_stream(dev))
+    nbytes = attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs)
+    gbs = nbytes / sec / 1e9
+    log(f"cfg5 attention: {sec * 1e6:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
+    return {"workload": "cfg5 paged MQA decode attention: batch 256, Hq 32, Hkv 1, D 128, bf16, "
+                        "lognormal ctx mean 1024 cap 8192 (seed 0), bs 16, fragmented tables",
+            "sum_kv": int(p.lens.sum()), "us_per_launch": sec * 1e6,
+            "bytes_per_launch": nbytes, "achieved_gbs": gbs,
+            "frac_of_peak": gbs / HBM_PEAK_GBS, "target_frac": 0.70}
+
+
+def run_cpu_baseline(hot, torch):
+    """The reference's PyTorch paged path (oracle.torch_ref: per-sequence
+    index_select gather + scaled_dot_product_attention, as in the
+    reference's tests/test.py:145-178) on the host CPU, bf16 as in the GPU
+    workload, over a bounded sample: one layer, the first 16 sequences of
+    the config-4 batch, repeated for about 10 s."""
+    from oracle import torch_ref
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    pool = hot["pool"]
+    kp = pool.kv[0, 0].cpu()
+    vp = pool.kv[0, 1].cpu()
+    q = hot["q"][:16].cpu()
+    lens = [int(x) + 1 for x in hot["lens"][:16]]
+    tables = hot["tables"][:16]
+    nbytes = attn_bytes(lens, q.shape[1], 1, q.shape[2], 2, pool.block_size)
+    for _ in range(2):
+        torch_ref.paged_attention_sdpa(q, kp, vp, tables, lens)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        torch_ref.paged_attention_sdpa(q, kp, vp, tables, lens)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 2000:
+            break
+    sec = el / reps
+    gbs = nbytes / sec / 1e9
+    log(f"cpu baseline: {sec * 1e3:.2f} ms per sample, {gbs:.3f} GB/s on {threads} threads")
+    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"1 layer, 16 of the 128 config-4 sequences (sum kv {sum(lens)}), bf16, "
+                      f"{reps} repetitions over {el:.1f} s; torch gather + SDPA "
+                      "(oracle/torch_ref.paged_attention_sdpa)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--model-steps", type=int, default=30)
+    ap.add_argument("--no-model", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-north-star", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
+              "(sequences shard by data parallelism with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    from serving import _native
+    _native.lib()
+
+    hot = run_hot_path(args, torch)
+    value = hot["step_bytes"] / hot["step_sec"] / 1e9
+    model = None if args.no_model else run_model(args, torch)
+    ns = None if args.no_north_star else run_north_star(args, torch)
+    cpu = None if args.no_cpu else run_cpu_baseline(hot, torch)
+
+    achieved = hot["attn_bytes"] / hot["attn_sec"] / 1e9
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "traffic_cfg4_attention.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(hot["step_sec"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg4 paged decode step: 12 layers x (slot-mapped KV append of 128 rows + "
+                        "paged MQA decode attention), batch 128, Hq 16, Hkv 1, D 64, ctx "
+                        "U[256,2048] seed 0, block_size 16, 16384-block pool per layer",
+            "global_batch": 128,
+            "layers": 12,
+            "step_bytes": hot["step_bytes"],
+            "parallelism": "none (1 GPU)",
+        },
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "decode_tok_s": None if model is None else round(model["tok_s"], 1),
+        "decode_step_ms": None if model is None else round(model["step_sec"] * 1e3, 4),
+        "roofline": {
+            "kernel": "paged MQA decode attention (cfg4, one layer)",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": hot["attn_bytes"],
+            "us_per_launch": round(hot["attn_sec"] * 1e6, 3),
+        },
+        "north_star": ns,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,152 @@
+/*
+ * pagedkv.h — C ABI of libpagedkv.so, the MI355X (gfx950) paged KV-cache
+ * decode path: slot-mapped K/V append into a block pool, block-table gather,
+ * and paged (multi-query) attention with split-K over the context.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers unless stated otherwise. The caller
+ *     owns every buffer (outputs, workspace, status word); nothing here
+ *     allocates device memory.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Work is enqueued asynchronously; no entry point synchronises the host.
+ *   - Return value: PKV_OK (0) or a negative PKV_ERR_* code; the message of
+ *     the last failure on the calling thread is pkv_last_error().
+ *   - `dtype` is one of PKV_DTYPE_*; K/V/Q/out share it.
+ *   - Pool layout (per layer, per K or V): [num_blocks, block_size, hkv, d]
+ *     contiguous, i.e. token slot `s` starts at element s * hkv * d.
+ *   - `status` (nullable) is a device int32 word the kernels OR error bits
+ *     into (PKV_STATUS_*) instead of touching memory out of bounds; the caller
+ *     zeroes it and reads it whenever it chooses to synchronise.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository
+ * akshay919191/tiny-transformer-inference-engine):
+ *   pkv_append            KVPool.write              serving/kv_pool.py:57-70
+ *   pkv_append_from_table KVPool.make_slot_mapping + write, looped per
+ *                         sequence in MQA_Paged.forward_paged_batched
+ *                                                    serving/kv_pool.py:40-55,
+ *                                                    serving/paged_mqa.py:87-99
+ *   pkv_gather            KVPool.gather             serving/kv_pool.py:72-82
+ *   pkv_paged_attention   pagedattn.paged_attn_fwd  kernels/pagedattn/extension.cpp:56-69
+ *                         (paged_attn_fwd_cuda      kernels/pagedattn/pagedattn.cu:1052-1079)
+ *   pkv_attention_workspace_bytes  no counterpart: the reference kernel has no
+ *                         split-K and therefore no workspace.
+ */
+#ifndef PAGEDKV_H
+#define PAGEDKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKV_VERSION 1
+
+#define PKV_DTYPE_F32 0
+#define PKV_DTYPE_F16 1
+#define PKV_DTYPE_BF16 2
+
+#define PKV_OK 0
+#define PKV_ERR_INVALID (-1)     /* bad argument (shape, null pointer, ...) */
+#define PKV_ERR_UNSUPPORTED (-2) /* valid but unsupported configuration   */
+#define PKV_ERR_WORKSPACE (-3)   /* workspace missing or too small         */
+#define PKV_ERR_HIP (-4)         /* a HIP runtime call failed              */
+
+/* Bits OR-ed into *status by the kernels. */
+#define PKV_STATUS_BAD_SLOT 1    /* append: slot outside [-slots, slots)   */
+#define PKV_STATUS_BAD_BLOCK 2   /* a block-table entry outside [0, num_blocks)
+                                    (or block 0 for an append) was skipped */
+#define PKV_STATUS_SHORT_TABLE 4 /* append: position beyond the table      */
+
+/* Library version (PKV_VERSION). */
+int pkv_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* pkv_last_error(void);
+
+/*
+ * Slot-mapped scatter: for t in [0, n_tok):
+ *   k_pool[slot(t)] = k_new[t];  v_pool[slot(t)] = v_new[t]
+ * where a row is `row_elems` (= hkv * d) contiguous elements and
+ * slot(t) = slot_mapping[t] (int64), wrapped by pool_slots when negative
+ * (index_put semantics). Slots outside [-pool_slots, pool_slots) are skipped
+ * and flagged PKV_STATUS_BAD_SLOT. Bit-exact copy.
+ * Replaces KVPool.write (serving/kv_pool.py:57-70).
+ */
+int pkv_append(void* k_pool, void* v_pool, int64_t pool_slots,
+               const void* k_new, const void* v_new,
+               const int64_t* slot_mapping, int64_t n_tok, int64_t row_elems,
+               int dtype, int* status, void* stream);
+
+/*
+ * Append with the slot computed in-kernel from device metadata. Token t of
+ * sequence s (query_start_loc[s] <= t < query_start_loc[s+1]) sits at
+ * position p = start_pos[s] + (t - query_start_loc[s]) and goes to slot
+ *   block_tables[s * max_blk + p / block_size] * block_size + p % block_size.
+ * A position beyond max_blk blocks (PKV_STATUS_SHORT_TABLE) or a physical
+ * block outside [1, num_blocks) (PKV_STATUS_BAD_BLOCK; block 0 is reserved)
+ * is skipped. Same result as make_slot_mapping + write per sequence.
+ * Replaces serving/kv_pool.py:40-70 as looped in serving/paged_mqa.py:87-99.
+ */
+int pkv_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
+                          int block_size, const void* k_new, const void* v_new,
+                          const int32_t* block_tables, int max_blk,
+                          const int32_t* query_start_loc,
+                          const int32_t* start_pos, int n_seq, int64_t n_tok,
+                          int64_t row_elems, int dtype, int* status,
+                          void* stream);
+
+/*
+ * Gather one sequence's first seq_len token rows out of the pool into dense
+ * k_out/v_out [seq_len, row_elems] following block_table (device int32,
+ * n_blocks entries). Replaces KVPool.gather (serving/kv_pool.py:72-82).
+ */
+int pkv_gather(void* k_out, void* v_out, const void* k_pool,
+               const void* v_pool, int64_t num_blocks, int block_size,
+               const int32_t* block_table, int n_blocks, int seq_len,
+               int64_t row_elems, int dtype, int* status, void* stream);
+
+/*
+ * Bytes of workspace pkv_paged_attention needs for this problem (0 when no
+ * sequence is split). `max_kv_len` <= 0 means max_blk * block_size.
+ */
+size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
+                                     int d, int max_blk, int block_size,
+                                     int max_kv_len, int part_tokens,
+                                     int dtype);
+
+/*
+ * Paged attention forward, semantics of pagedattn.paged_attn_fwd
+ * (kernels/pagedattn/pagedattn.cu:142-447, host side :1052-1079):
+ *   q   [T, hq, d]; out [T, hq, d]; lse (nullable) float [T, hq]
+ *   k_pool/v_pool [num_blocks, block_size, hkv, d]
+ *   block_tables int32 [n_seq, max_blk]; seq_lens int32 [n_seq]
+ *   query_start_loc int32 [n_seq + 1] (NULL = one query per sequence,
+ *   token s belongs to sequence s: the decode case)
+ * For sequence s: kv_len = min(seq_lens[s], max_blk * block_size),
+ * q_len = query_start_loc[s+1] - query_start_loc[s],
+ * ctx = causal ? max(kv_len - q_len, 0) : 0; query i sees key j iff
+ * j < kv_len and (!causal or j <= ctx + i). Query head h reads kv head
+ * h / (hq / hkv). scale <= 0 means 1/sqrt(d). Rows with no visible key give
+ * out = 0 and lse = +inf. lse = m + ln(l) in natural-log units.
+ * `max_q_len` must bound every q_len; `max_kv_len` (<= 0: the table
+ * capacity) must bound every kv_len; `part_tokens` (0: automatic) is the
+ * split-K partition length. Workspace: pkv_attention_workspace_bytes().
+ */
+int pkv_paged_attention(void* out, float* lse, const void* q,
+                        const void* k_pool, const void* v_pool,
+                        int64_t num_blocks, int block_size,
+                        const int32_t* block_tables, int max_blk,
+                        const int32_t* seq_lens,
+                        const int32_t* query_start_loc, int n_seq,
+                        int max_q_len, int max_kv_len, int hq, int hkv, int d,
+                        float scale, int causal, int part_tokens, int dtype,
+                        void* workspace, size_t workspace_bytes, int* status,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDKV_H */

@@ -1,0 +1,355 @@
+// Paged attention forward for gfx950: block-table gather fused with
+// QK^T, online softmax and PV, split-K over the context with a merge pass.
+//
+// Semantics follow pagedattn.forward (kernels/pagedattn/pagedattn.cu:142-447):
+//   kv_len = min(seq_lens[s], max_blk * bs)                       (:187-189)
+//   ctx    = causal ? max(kv_len - q_len, 0) : 0                   (:196-200)
+//   query i sees key j iff j < kv_len and (!causal or j <= ctx+i) (:315-329)
+//   kv head = q head / (hq / hkv)                                  (:180)
+//   rows with no visible key: out = 0, lse = +inf                  (:418-446)
+// but nothing of its structure: there the grid is one CTA per (sequence,
+// query head, 64-query tile), each re-streaming the whole context. Here a
+// workgroup owns a tile of (query token, head) ROWS that share one kv head,
+// so every K/V token is staged once per tile and reused by every query head
+// of the group (for decode, one tile holds all heads of the group), and the
+// context is cut into partitions that run as separate workgroups (split-K);
+// a merge kernel combines the partial (max, sum, output) triples.
+//
+// Softmax runs in base 2: scores are scaled by scale*log2(e) and
+// exponentiated with exp2, so the running max m and lse are converted back
+// with ln(2) only at the end.
+#include "pkv_internal.h"
+
+#include <math.h>
+
+namespace pkv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr float kLn2 = 0.6931471805599453f;
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T x) {
+  return (float)x;
+}
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+  return (T)x;
+}
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Per-(sequence, kv head, row tile) geometry shared by the attention and
+// merge kernels; both must derive the same partition count.
+struct TileGeom {
+  int q_begin, q_len, rows_here, kv_len, ctx, kv_limit, part_len, nparts;
+};
+
+__device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
+                                          int rows_per_tile, TileGeom& g) {
+  g.q_begin = a.qloc ? a.qloc[s] : s;
+  g.q_len = a.qloc ? a.qloc[s + 1] - g.q_begin : 1;
+  const int rows_total = g.q_len * a.group;
+  const int r0 = tile * rows_per_tile;
+  if (g.q_len <= 0 || r0 >= rows_total) return false;
+  g.rows_here = min(rows_per_tile, rows_total - r0);
+  int kv_len = a.seq_lens[s];
+  const int cap = a.max_blk << a.bs_shift;
+  kv_len = kv_len < cap ? kv_len : cap;
+  g.kv_len = kv_len > 0 ? kv_len : 0;
+  g.ctx = a.causal ? max(g.kv_len - g.q_len, 0) : 0;
+  g.kv_limit = g.kv_len;
+  if (a.causal) {
+    const int i_last = (r0 + g.rows_here - 1) / a.group;
+    g.kv_limit = min(g.kv_limit, g.ctx + i_last + 1);
+  }
+  // A sequence longer than the planned bound still gets every key: its
+  // partitions grow so that their count never exceeds the grid.
+  int plen = a.part_tokens;
+  if (ceil_div(g.kv_limit, plen) > a.parts_max)
+    plen = ceil_div(ceil_div(g.kv_limit, a.parts_max), kChunk) * kChunk;
+  g.part_len = plen;
+  g.nparts = max(1, ceil_div(g.kv_limit, plen));
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel: any dtype, any group size, any q_len, d <= DMAX.
+// 256 threads; thread t owns row t/8 and, within it, keys (t%8)+8e of each
+// 32-key chunk for QK and output columns (t%8)+8j for PV. Row max / sum
+// reductions are 8-lane shuffles inside one wavefront.
+// ---------------------------------------------------------------------------
+template <typename T, int DMAX>
+__global__ __launch_bounds__(kThreads) void attn_rows_kernel(AttnArgs a) {
+  constexpr int R = kGenRows;
+  constexpr int C = kChunk;
+  constexpr int DP = DMAX + 1;  // odd pitch: row-strided reads hit distinct banks
+  constexpr int NJ = DMAX / 8;
+  __shared__ float Qs[R][DP];
+  __shared__ float Ks[C][DP];
+  __shared__ float Vs[C][DP];
+  __shared__ float Ps[R][C + 1];
+
+  const int tid = threadIdx.x;
+  const int part = blockIdx.x;
+  const int tile = blockIdx.y;
+  const int s = blockIdx.z / a.hkv;
+  const int kvh = blockIdx.z - s * a.hkv;
+  TileGeom g;
+  if (!tile_geom(a, s, tile, R, g)) return;
+  if (part >= g.nparts) return;
+  const int D = a.d;
+  const int G = a.group;
+  const int r0 = tile * R;
+  const int kv_lo = part * g.part_len;
+  const int kv_hi = min(kv_lo + g.part_len, g.kv_limit);
+
+  const T* __restrict__ q = static_cast<const T*>(a.q);
+  const T* __restrict__ kp = static_cast<const T*>(a.k_pool);
+  const T* __restrict__ vp = static_cast<const T*>(a.v_pool);
+  const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
+  const int bs_mask = (1 << a.bs_shift) - 1;
+
+  for (int idx = tid; idx < R * D; idx += kThreads) {
+    const int r = idx / D;
+    const int dd = idx - r * D;
+    float v = 0.f;
+    if (r < g.rows_here) {
+      const int rg = r0 + r;
+      const int i = rg / G;
+      const int h = rg - i * G;
+      const int64_t qrow = (int64_t)(g.q_begin + i) * a.hq + kvh * G + h;
+      v = to_f32(q[qrow * D + dd]);
+    }
+    Qs[r][dd] = v;
+  }
+
+  const int r = tid >> 3;
+  const int c8 = tid & 7;
+  const bool row_valid = r < g.rows_here;
+  int vis_hi = kv_hi;
+  if (a.causal) vis_hi = min(vis_hi, g.ctx + (r0 + r) / G + 1);
+
+  float m = -INFINITY, l = 0.f;
+  float o[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) o[j] = 0.f;
+
+  for (int c0 = kv_lo; c0 < kv_hi; c0 += C) {
+    __syncthreads();
+    for (int idx = tid; idx < C * D; idx += kThreads) {
+      const int t = idx / D;
+      const int dd = idx - t * D;
+      const int pos = c0 + t;
+      float kv_k = 0.f, kv_v = 0.f;
+      if (pos < kv_hi) {
+        const int64_t phys = table[pos >> a.bs_shift];
+        if (phys >= 0 && phys < a.num_blocks) {
+          const int64_t off =
+              (((phys << a.bs_shift) + (pos & bs_mask)) * a.hkv + kvh) * D + dd;
+          kv_k = to_f32(kp[off]);
+          kv_v = to_f32(vp[off]);
+        } else if (a.status && dd == 0) {
+          atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
+        }
+      }
+      Ks[t][dd] = kv_k;
+      Vs[t][dd] = kv_v;
+    }
+    __syncthreads();
+
+    float sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = c8 + 8 * e;
+      float acc = 0.f;
+      for (int dd = 0; dd < D; ++dd) acc = fmaf(Qs[r][dd], Ks[j][dd], acc);
+      const bool vis = row_valid && (c0 + j) < vis_hi;
+      sc[e] = vis ? acc * a.scale_log2 : -INFINITY;
+      mx = fmaxf(mx, sc[e]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 8));
+    const float m_new = fmaxf(m, mx);
+    const float ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m - ref);
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = exp2f(sc[e] - ref);
+      Ps[r][c8 + 8 * e] = p;
+      psum += p;
+    }
+    psum += __shfl_xor(psum, 1, 8);
+    psum += __shfl_xor(psum, 2, 8);
+    psum += __shfl_xor(psum, 4, 8);
+    l = l * alpha + psum;
+    m = m_new;
+    __syncthreads();
+#pragma unroll
+    for (int jd = 0; jd < NJ; ++jd) {
+      const int dd = c8 + 8 * jd;
+      if (dd < D) {
+        float acc = o[jd] * alpha;
+        for (int j = 0; j < C; ++j) acc = fmaf(Ps[r][j], Vs[j][dd], acc);
+        o[jd] = acc;
+      }
+    }
+  }
+
+  if (!row_valid) return;
+  const int rg = r0 + r;
+  const int i = rg / G;
+  const int h = rg - i * G;
+  const int64_t qrow = (int64_t)(g.q_begin + i) * a.hq + kvh * G + h;
+  if (g.nparts == 1) {
+    T* __restrict__ out = static_cast<T*>(a.out);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int jd = 0; jd < NJ; ++jd) {
+      const int dd = c8 + 8 * jd;
+      if (dd < D) out[qrow * D + dd] = from_f32<T>(o[jd] * inv);
+    }
+    if (a.lse && c8 == 0) a.lse[qrow] = l > 0.f ? (m + log2f(l)) * kLn2 : INFINITY;
+  } else {
+    const int64_t unit =
+        ((int64_t)blockIdx.z * a.tiles_max + tile) * a.parts_max + part;
+    float* __restrict__ wo = a.ws_o + (unit * R + r) * D;
+#pragma unroll
+    for (int jd = 0; jd < NJ; ++jd) {
+      const int dd = c8 + 8 * jd;
+      if (dd < D) wo[dd] = o[jd];
+    }
+    if (c8 == 0) {
+      a.ws_ml[(unit * R + r) * 2 + 0] = m;
+      a.ws_ml[(unit * R + r) * 2 + 1] = l;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K merge: for every row of a tile that was split, combine the
+// partitions' (m_p, l_p, o_p): M = max m_p, w_p = 2^(m_p - M),
+// out = sum w_p o_p / sum w_p l_p, lse = (M + log2 sum w_p l_p) ln 2.
+// Grid (tiles, n_seq * hkv); thread t owns row t / 8, columns (t%8) + 8j.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a,
+                                                         int rows_per_tile) {
+  const int tile = blockIdx.x;
+  const int s = blockIdx.y / a.hkv;
+  const int kvh = blockIdx.y - s * a.hkv;
+  TileGeom g;
+  if (!tile_geom(a, s, tile, rows_per_tile, g)) return;
+  if (g.nparts == 1) return;
+  const int D = a.d;
+  const int G = a.group;
+  const int r0 = tile * rows_per_tile;
+  const int64_t unit0 = ((int64_t)blockIdx.y * a.tiles_max + tile) * a.parts_max;
+  T* __restrict__ out = static_cast<T*>(a.out);
+  const int lanes_per_row = kThreads / rows_per_tile;
+  for (int r = threadIdx.x / lanes_per_row; r < g.rows_here;
+       r += kThreads / lanes_per_row) {
+    const int c = threadIdx.x % lanes_per_row;
+    float M = -INFINITY;
+    for (int p = 0; p < g.nparts; ++p)
+      M = fmaxf(M, a.ws_ml[((unit0 + p) * rows_per_tile + r) * 2]);
+    const int rg = r0 + r;
+    const int i = rg / G;
+    const int h = rg - i * G;
+    const int64_t qrow = (int64_t)(g.q_begin + i) * a.hq + kvh * G + h;
+    if (M == -INFINITY) {
+      for (int dd = c; dd < D; dd += lanes_per_row) out[qrow * D + dd] = from_f32<T>(0.f);
+      if (a.lse && c == 0) a.lse[qrow] = INFINITY;
+      continue;
+    }
+    float L = 0.f;
+    for (int p = 0; p < g.nparts; ++p) {
+      const float* ml = a.ws_ml + ((unit0 + p) * rows_per_tile + r) * 2;
+      L += ml[1] * exp2f(ml[0] - M);
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    for (int dd = c; dd < D; dd += lanes_per_row) {
+      float acc = 0.f;
+      for (int p = 0; p < g.nparts; ++p) {
+        const int64_t row = (unit0 + p) * rows_per_tile + r;
+        acc = fmaf(a.ws_o[row * D + dd], exp2f(a.ws_ml[row * 2] - M), acc);
+      }
+      out[qrow * D + dd] = from_f32<T>(acc * inv);
+    }
+    if (a.lse && c == 0) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2 : INFINITY;
+  }
+}
+
+template <typename T>
+int launch_generic(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
+  const dim3 grid(p.parts_max, p.tiles_max, a.n_seq * a.hkv);
+  if (a.d <= 64) {
+    hipLaunchKernelGGL((attn_rows_kernel<T, 64>), grid, dim3(kThreads), 0, stream, a);
+  } else if (a.d <= 128) {
+    hipLaunchKernelGGL((attn_rows_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((attn_rows_kernel<T, 256>), grid, dim3(kThreads), 0, stream, a);
+  }
+  int rc = check_launch("attn_rows_kernel");
+  if (rc != PKV_OK || p.parts_max == 1) return rc;
+  hipLaunchKernelGGL((merge_kernel<T>), dim3(p.tiles_max, a.n_seq * a.hkv),
+                     dim3(kThreads), 0, stream, a, p.rows);
+  return check_launch("merge_kernel");
+}
+
+int ceil_div_h(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+}  // namespace
+
+AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
+                        int max_blk, int block_size, int max_kv_len,
+                        int part_tokens, int dtype) {
+  (void)dtype;
+  AttnPlan p{};
+  const int group = hq / hkv;
+  p.kind = 0;
+  p.rows = kGenRows;
+  p.tiles_max = ceil_div_h((int64_t)max_q_len * group, p.rows);
+  if (p.tiles_max < 1) p.tiles_max = 1;
+  const int64_t cap = (int64_t)max_blk * block_size;
+  int64_t kvb = max_kv_len > 0 && max_kv_len < cap ? max_kv_len : cap;
+  if (kvb < 1) kvb = 1;
+  const int64_t units = (int64_t)n_seq * hkv * p.tiles_max;
+  int plen = part_tokens;
+  if (plen <= 0) {
+    // Aim for ~2048 workgroups so the 256 CUs stay busy even when most
+    // sequences are far below the bound.
+    int64_t parts_target = (2048 + units - 1) / (units > 0 ? units : 1);
+    if (parts_target < 1) parts_target = 1;
+    plen = (int)((kvb + parts_target - 1) / parts_target);
+    if (plen < 64) plen = 64;
+  }
+  plen = (plen + kChunk - 1) / kChunk * kChunk;
+  p.part_tokens = plen;
+  p.parts_max = ceil_div_h(kvb, plen);
+  if (p.parts_max < 1) p.parts_max = 1;
+  p.ws_bytes = p.parts_max > 1
+                   ? (size_t)units * p.parts_max * p.rows * ((size_t)d + 2) * sizeof(float)
+                   : 0;
+  return p;
+}
+
+int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
+                     hipStream_t stream) {
+  if (a.n_seq == 0) return PKV_OK;
+  if (p.parts_max > 65535 || p.tiles_max > 65535 ||
+      (int64_t)a.n_seq * a.hkv > 65535)
+    return fail(PKV_ERR_UNSUPPORTED, "attention grid too large (%d parts, %d tiles, %d seq*hkv)",
+                p.parts_max, p.tiles_max, a.n_seq * a.hkv);
+  switch (dtype) {
+    case PKV_DTYPE_F32: return launch_generic<float>(a, p, stream);
+    case PKV_DTYPE_F16: return launch_generic<f16>(a, p, stream);
+    case PKV_DTYPE_BF16: return launch_generic<bf16>(a, p, stream);
+  }
+  return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+}
+
+}  // namespace pkv

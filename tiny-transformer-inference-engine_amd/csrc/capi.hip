@@ -1,0 +1,196 @@
+// C ABI of libpagedkv.so (declared in include/pagedkv.h): argument
+// validation mirroring the reference's checks, then dispatch to the kernels.
+//
+// Validation follows check_paged_inputs (kernels/pagedattn/pagedattn.cu:867-895)
+// and paged_varlen_attention (serving/fake_paged_attn.py:171-198): head dim a
+// multiple of 8 and <= 256, hq a multiple of hkv, power-of-two block size.
+// Unlike the reference, f32 and bf16 are computed natively (the reference
+// casts everything to fp16, fake_paged_attn.py:208-215).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "pkv_internal.h"
+
+namespace pkv {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(PKV_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+  return PKV_OK;
+}
+
+static bool valid_dtype(int dtype) {
+  return dtype == PKV_DTYPE_F32 || dtype == PKV_DTYPE_F16 ||
+         dtype == PKV_DTYPE_BF16;
+}
+
+static int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
+}
+
+}  // namespace pkv
+
+using namespace pkv;
+
+extern "C" {
+
+int pkv_version(void) { return PKV_VERSION; }
+
+const char* pkv_last_error(void) { return g_err; }
+
+int pkv_append(void* k_pool, void* v_pool, int64_t pool_slots,
+               const void* k_new, const void* v_new,
+               const int64_t* slot_mapping, int64_t n_tok, int64_t row_elems,
+               int dtype, int* status, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  if (n_tok < 0 || row_elems <= 0 || pool_slots < 0)
+    return fail(PKV_ERR_INVALID, "bad sizes n_tok=%lld row_elems=%lld pool_slots=%lld",
+                (long long)n_tok, (long long)row_elems, (long long)pool_slots);
+  if (n_tok == 0) return PKV_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping)
+    return fail(PKV_ERR_INVALID, "null pointer argument");
+  return launch_append(k_pool, v_pool, pool_slots, k_new, v_new, slot_mapping,
+                       n_tok, row_elems * elem_bytes(dtype), status,
+                       (hipStream_t)stream);
+}
+
+int pkv_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
+                          int block_size, const void* k_new, const void* v_new,
+                          const int32_t* block_tables, int max_blk,
+                          const int32_t* query_start_loc,
+                          const int32_t* start_pos, int n_seq, int64_t n_tok,
+                          int64_t row_elems, int dtype, int* status,
+                          void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  const int bs_shift = log2_exact(block_size);
+  if (bs_shift < 0)
+    return fail(PKV_ERR_INVALID, "blocksize %d must be a power of two", block_size);
+  if (n_tok < 0 || n_seq < 0 || row_elems <= 0 || max_blk < 0 || num_blocks < 0)
+    return fail(PKV_ERR_INVALID, "bad sizes");
+  if (n_tok == 0 || n_seq == 0) return PKV_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !block_tables ||
+      !query_start_loc || !start_pos)
+    return fail(PKV_ERR_INVALID, "null pointer argument");
+  return launch_append_from_table(
+      k_pool, v_pool, num_blocks, bs_shift, k_new, v_new, block_tables,
+      max_blk, query_start_loc, start_pos, n_seq, n_tok,
+      row_elems * elem_bytes(dtype), status, (hipStream_t)stream);
+}
+
+int pkv_gather(void* k_out, void* v_out, const void* k_pool,
+               const void* v_pool, int64_t num_blocks, int block_size,
+               const int32_t* block_table, int n_blocks, int seq_len,
+               int64_t row_elems, int dtype, int* status, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  const int bs_shift = log2_exact(block_size);
+  if (bs_shift < 0)
+    return fail(PKV_ERR_INVALID, "blocksize %d must be a power of two", block_size);
+  if (seq_len < 0 || n_blocks < 0 || row_elems <= 0)
+    return fail(PKV_ERR_INVALID, "bad sizes");
+  if ((int64_t)seq_len > (int64_t)n_blocks * block_size)
+    return fail(PKV_ERR_INVALID,
+                "seq_len=%d exceeds capacity of block_table (%lld)", seq_len,
+                (long long)n_blocks * block_size);
+  if (seq_len == 0) return PKV_OK;
+  if (!k_out || !v_out || !k_pool || !v_pool || !block_table)
+    return fail(PKV_ERR_INVALID, "null pointer argument");
+  return launch_gather(k_out, v_out, k_pool, v_pool, num_blocks, bs_shift,
+                       block_table, n_blocks, seq_len,
+                       row_elems * elem_bytes(dtype), status,
+                       (hipStream_t)stream);
+}
+
+size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
+                                     int d, int max_blk, int block_size,
+                                     int max_kv_len, int part_tokens,
+                                     int dtype) {
+  if (n_seq <= 0 || max_q_len <= 0 || hkv <= 0 || hq <= 0 || hq % hkv != 0)
+    return 0;
+  return plan_attention(n_seq, max_q_len, hq, hkv, d, max_blk, block_size,
+                        max_kv_len, part_tokens, dtype)
+      .ws_bytes;
+}
+
+int pkv_paged_attention(void* out, float* lse, const void* q,
+                        const void* k_pool, const void* v_pool,
+                        int64_t num_blocks, int block_size,
+                        const int32_t* block_tables, int max_blk,
+                        const int32_t* seq_lens,
+                        const int32_t* query_start_loc, int n_seq,
+                        int max_q_len, int max_kv_len, int hq, int hkv, int d,
+                        float scale, int causal, int part_tokens, int dtype,
+                        void* workspace, size_t workspace_bytes, int* status,
+                        void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  if (hkv <= 0 || hq <= 0 || hq % hkv != 0)
+    return fail(PKV_ERR_INVALID, "Hq (%d) must be a multiple of Hkv (%d)", hq, hkv);
+  if (d <= 0 || d % 8 != 0)
+    return fail(PKV_ERR_INVALID, "head_dim %d must be a multiple of 8", d);
+  if (d > 256) return fail(PKV_ERR_UNSUPPORTED, "head dim > 256 not supported");
+  const int bs_shift = log2_exact(block_size);
+  if (bs_shift < 0)
+    return fail(PKV_ERR_INVALID, "blocksize %d must be a power of two", block_size);
+  if (n_seq < 0 || max_blk < 0 || num_blocks < 0 || max_q_len < 0)
+    return fail(PKV_ERR_INVALID, "bad sizes");
+  if (n_seq == 0 || max_q_len == 0) return PKV_OK;
+  if (!out || !q || !k_pool || !v_pool || !seq_lens || (max_blk > 0 && !block_tables))
+    return fail(PKV_ERR_INVALID, "null pointer argument");
+  if (!query_start_loc && max_q_len != 1)
+    return fail(PKV_ERR_INVALID, "query_start_loc may be NULL only when max_q_len == 1");
+  const AttnPlan plan = plan_attention(n_seq, max_q_len, hq, hkv, d, max_blk,
+                                       block_size, max_kv_len, part_tokens,
+                                       dtype);
+  if (plan.ws_bytes > 0 && (!workspace || workspace_bytes < plan.ws_bytes))
+    return fail(PKV_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given",
+                plan.ws_bytes, workspace ? workspace_bytes : (size_t)0);
+  const float sc = scale > 0.f ? scale : 1.f / sqrtf((float)d);
+  AttnArgs a{};
+  a.out = out;
+  a.lse = lse;
+  a.q = q;
+  a.k_pool = k_pool;
+  a.v_pool = v_pool;
+  a.block_tables = block_tables;
+  a.seq_lens = seq_lens;
+  a.qloc = query_start_loc;
+  a.num_blocks = num_blocks;
+  a.bs_shift = bs_shift;
+  a.max_blk = max_blk;
+  a.n_seq = n_seq;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.group = hq / hkv;
+  a.d = d;
+  a.scale_log2 = sc * 1.4426950408889634f;
+  a.causal = causal ? 1 : 0;
+  a.part_tokens = plan.part_tokens;
+  a.parts_max = plan.parts_max;
+  a.tiles_max = plan.tiles_max;
+  float* ws = static_cast<float*>(workspace);
+  const size_t units = (size_t)n_seq * hkv * plan.tiles_max * plan.parts_max;
+  a.ws_o = plan.ws_bytes ? ws : nullptr;
+  a.ws_ml = plan.ws_bytes ? ws + units * plan.rows * (size_t)d : nullptr;
+  a.status = status;
+  return launch_attention(a, plan, dtype, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,140 @@
+"""ctypes binding of libpagedkv.so (the HIP kernels behind the C ABI in
+include/pagedkv.h).
+
+The library is required: every function here raises RuntimeError when it is
+missing or when a tensor is not on a ROCm device. There is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libpagedkv.so")
+
+DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+PKV_STATUS_BAD_SLOT = 1
+PKV_STATUS_BAD_BLOCK = 2
+PKV_STATUS_SHORT_TABLE = 4
+
+_lib = None
+_lock = threading.Lock()
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_vp = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+_c_float = ctypes.c_float
+
+_SIGNATURES = {
+    "pkv_version": ([], _c_int),
+    "pkv_last_error": ([], ctypes.c_char_p),
+    "pkv_append": ([_c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                    _c_int, _c_vp, _c_vp], _c_int),
+    "pkv_append_from_table": ([_c_vp, _c_vp, _c_i64, _c_int, _c_vp, _c_vp,
+                               _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_i64,
+                               _c_i64, _c_int, _c_vp, _c_vp], _c_int),
+    "pkv_gather": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_vp, _c_int,
+                    _c_int, _c_i64, _c_int, _c_vp, _c_vp], _c_int),
+    "pkv_attention_workspace_bytes": ([_c_int, _c_int, _c_int, _c_int, _c_int,
+                                       _c_int, _c_int, _c_int, _c_int, _c_int],
+                                      _c_size),
+    "pkv_paged_attention": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int,
+                             _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int,
+                             _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
+                             _c_int, _c_int, _c_vp, _c_size, _c_vp, _c_vp],
+                            _c_int),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+def lib():
+    """Load (once) and return the ctypes handle of libpagedkv.so."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"libpagedkv.so not found at {LIB_PATH}; build it with "
+                    "`python tiny-transformer-inference-engine_amd/build_native.py` "
+                    "(or __graft_entry__.build())")
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in _SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = handle
+    return _lib
+
+
+def is_available() -> bool:
+    """True when the library loads and a ROCm device is visible."""
+    try:
+        lib()
+    except (RuntimeError, OSError):
+        return False
+    return torch.cuda.is_available()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().pkv_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(f"{what}: {msg}")
+        if rc == -2:
+            raise NotImplementedError(f"{what}: {msg}")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def require_device(*tensors: torch.Tensor, what: str = "paged kv op") -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                f"{what} requires tensors on a ROCm GPU device (got {t.device}); "
+                "the HIP library has no CPU path")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16")
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class Workspace:
+    """Per-device scratch for split-K partials, grown on demand and reused
+    (the library never allocates). Allocation goes through torch's caching
+    allocator, so it is stream-ordered on the current stream."""
+
+    def __init__(self):
+        self._bufs: dict[int, torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        buf = self._bufs.get(idx)
+        if buf is None or buf.numel() < nbytes:
+            # grow geometrically so ragged batches do not reallocate every step
+            size = max(nbytes, 0 if buf is None else 2 * buf.numel())
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            self._bufs[idx] = buf
+        return buf
+
+
+WORKSPACE = Workspace()

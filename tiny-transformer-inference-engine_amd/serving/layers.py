@@ -1,0 +1,126 @@
+"""Dense layers around the paged attention path (they stay PyTorch ops).
+
+Each keeps the reference module's constructor, parameter names and
+arithmetic so that state dicts load unchanged and results match:
+  RoPE            models/rope.py:5-47 (interleaved even/odd pairs)
+  RMSNorm         models/rmsnorm.py:6-18 (the fp32 formula of its CPU branch)
+  SwiGLU          models/mlp.py:17-32 (silu(gate) * up, then down)
+  TokenEmbedding  models/embedding.py:5-15
+  ModelConfig     models/model_config.py:8-41
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+class RoPE(nn.Module):
+    """Rotary embedding on interleaved (even, odd) pairs:
+    out_even = x_even*cos - x_odd*sin, out_odd = x_even*sin + x_odd*cos with
+    angle position * base^(-2i/dim)."""
+
+    def __init__(self, dim, max_seq_len=2048, base=10000.0):
+        super().__init__()
+        assert dim % 2 == 0, "RoPE dimension must be even"
+        self.dim = dim
+        self.base = base
+        self.max_seq_len = max_seq_len
+        inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2).float() / dim))
+        angles = torch.outer(torch.arange(max_seq_len).float(), inv_freq)
+        # [1, 1, max_seq_len, dim/2], non-persistent like the reference
+        self.register_buffer("cos", angles.cos()[None, None], persistent=False)
+        self.register_buffer("sin", angles.sin()[None, None], persistent=False)
+
+    @staticmethod
+    def _rotate(q, k, cos, sin):
+        def rot(x):
+            y = torch.empty_like(x)
+            xe, xo = x[..., 0::2], x[..., 1::2]
+            y[..., 0::2] = xe * cos - xo * sin
+            y[..., 1::2] = xe * sin + xo * cos
+            return y
+        return rot(q), rot(k)
+
+    def forward(self, q, k, position_offset: int = 0):
+        T = q.shape[-2]
+        cos = self.cos[:, :, position_offset:position_offset + T, :].to(dtype=q.dtype)
+        sin = self.sin[:, :, position_offset:position_offset + T, :].to(dtype=q.dtype)
+        return self._rotate(q, k, cos, sin)
+
+    def forward_at(self, q, k, positions):
+        """q, k [..., H, T, D] rotated at absolute `positions` [T]."""
+        cos = self.cos.index_select(2, positions).to(dtype=q.dtype)
+        sin = self.sin.index_select(2, positions).to(dtype=q.dtype)
+        return self._rotate(q, k, cos, sin)
+
+    def forward_tokens(self, q, k, positions):
+        """Token-major variant: q [T, Hq, D], k [T, Hkv, D]. Same element-wise
+        arithmetic as forward_at, without the head/token transposes."""
+        cos = self.cos[0, 0].index_select(0, positions).to(dtype=q.dtype)[:, None, :]
+        sin = self.sin[0, 0].index_select(0, positions).to(dtype=q.dtype)[:, None, :]
+        return self._rotate(q, k, cos, sin)
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x32 = x.float()
+        y = x32 * torch.rsqrt(x32.square().mean(dim=-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(dtype=x.dtype)
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, d_model, hidden_dim, bias=False):
+        super().__init__()
+        self.gate_proj = nn.Linear(d_model, hidden_dim, bias=bias)
+        self.up_proj = nn.Linear(d_model, hidden_dim, bias=bias)
+        self.down_proj = nn.Linear(hidden_dim, d_model, bias=bias)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class TokenEmbedding(nn.Module):
+    def __init__(self, vocab_size, embed_dim):
+        super().__init__()
+        self.embedding = nn.Embedding(vocab_size, embed_dim)
+
+    def forward(self, x):
+        return self.embedding(x)
+
+
+@dataclass
+class ModelConfig:
+    vocab_size: int = 50257
+    d_model: int = 512
+    num_layers: int = 34
+    num_heads: int = 8
+    num_kv_heads: int = 1
+    max_seq_len: int = 512
+    causal: bool = True
+    dropout: float = 0.0
+    bias: bool = False
+    dtype: torch.dtype = torch.float32
+    eos_token_id: int = 50256
+    rope_theta: float = 10000.0
+    rms_norm_eps: float = 1e-5
+
+    def __post_init__(self):
+        assert self.d_model % self.num_heads == 0
+        assert self.num_heads % self.num_kv_heads == 0
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.num_heads
+
+    @property
+    def hidden_size(self) -> int:
+        # the reference's MLP width equals d_model (model_config.py:32-34)
+        return self.d_model

@@ -1,0 +1,58 @@
+"""Token sampling used by the Scheduler (reference: sampling.py:5-137).
+
+greedy = argmax; sample = temperature, then top-k (keep logits >= the k-th
+largest), then top-p (keep the smallest prefix of the sorted distribution
+whose mass reaches top_p, always at least one token), then a multinomial
+draw. Errors mirror the reference's ValueErrors.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def greedy(logits):
+    return torch.argmax(logits, dim=-1, keepdim=True)
+
+
+def apply_top_k(logits, top_k):
+    if top_k <= 0:
+        return logits
+    k = min(top_k, logits.shape[-1])
+    kth = torch.topk(logits.float(), k, dim=-1).values[:, -1:]
+    return logits.masked_fill(logits < kth, float("-inf"))
+
+
+def apply_top_p(logits, top_p):
+    if top_p >= 1.0:
+        return logits
+    if top_p <= 0.0:
+        raise ValueError("top_p must be > 0")
+    sorted_logits, order = torch.sort(logits, descending=True, dim=-1)
+    mass_before = torch.cumsum(F.softmax(sorted_logits, dim=-1), dim=-1)
+    # drop a token when the mass strictly before it already exceeds top_p
+    drop = torch.zeros_like(mass_before, dtype=torch.bool)
+    drop[:, 1:] = mass_before[:, :-1] > top_p
+    sorted_logits = sorted_logits.masked_fill(drop, float("-inf"))
+    return torch.full_like(logits, float("-inf")).scatter(-1, order, sorted_logits)
+
+
+def sample(logits, temperature=1.0, top_k=0, top_p=1.0):
+    if logits.ndim != 2 or logits.shape[-1] == 0:
+        raise ValueError("logits must have shape [batch, vocab] with non-empty vocab")
+    if not math.isfinite(temperature) or temperature <= 0:
+        raise ValueError("temperature must be finite and > 0")
+    if top_k < 0:
+        raise ValueError("top_k must be >= 0")
+    if not 0 < top_p <= 1:
+        raise ValueError("top_p must be in (0, 1]")
+    logits = logits.float()
+    if not torch.isfinite(logits).all():
+        raise ValueError("logits contain NaN or infinity")
+    logits = apply_top_p(apply_top_k(logits / temperature, top_k), top_p)
+    probs = F.softmax(logits, dim=-1)
+    if not torch.isfinite(probs).all() or (probs.sum(dim=-1) <= 0).any():
+        raise ValueError("sampling produced an invalid probability distribution")
+    return torch.multinomial(probs, num_samples=1)
