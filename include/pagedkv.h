@@ -58,6 +58,7 @@ extern "C" {
 #define PKV_STATUS_BAD_BLOCK 2   /* a block-table entry outside [0, num_blocks)
                                     (or block 0 for an append) was skipped */
 #define PKV_STATUS_SHORT_TABLE 4 /* append: position beyond the table      */
+#define PKV_STATUS_BAD_QLOC 8    /* attention: query range outside [0, T)  */
 
 /* Library version (PKV_VERSION). */
 int pkv_version(void);
@@ -123,7 +124,9 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
  *   k_pool/v_pool [num_blocks, block_size, hkv, d]
  *   block_tables int32 [n_seq, max_blk]; seq_lens int32 [n_seq]
  *   query_start_loc int32 [n_seq + 1] (NULL = one query per sequence,
- *   token s belongs to sequence s: the decode case)
+ *   token s belongs to sequence s: the decode case); n_tokens = T. A
+ *   sequence whose query range falls outside [0, T) is skipped and flagged
+ *   PKV_STATUS_BAD_QLOC.
  * For sequence s: kv_len = min(seq_lens[s], max_blk * block_size),
  * q_len = query_start_loc[s+1] - query_start_loc[s],
  * ctx = causal ? max(kv_len - q_len, 0) : 0; query i sees key j iff
@@ -140,7 +143,8 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
                         const int32_t* block_tables, int max_blk,
                         const int32_t* seq_lens,
                         const int32_t* query_start_loc, int n_seq,
-                        int max_q_len, int max_kv_len, int hq, int hkv, int d,
+                        int n_tokens, int max_q_len, int max_kv_len, int hq,
+                        int hkv, int d,
                         float scale, int causal, int part_tokens, int dtype,
                         void* workspace, size_t workspace_bytes, int* status,
                         void* stream);

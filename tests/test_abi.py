@@ -43,23 +43,23 @@ def test_validation_errors_without_gpu():
     L = _native.lib()
     # bad dtype, non-power-of-two block size, head dim not a multiple of 8,
     # hq not a multiple of hkv: all rejected on the host
-    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 0,
+    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 1, 0,
                                8, 1, 64, 0.0, 1, 0, 9, None, 0, None, None)
     assert rc == -1 and b"dtype" in L.pkv_last_error()
-    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 12, 1, 1, 1, None, 1, 1, 0,
+    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 12, 1, 1, 1, None, 1, 1, 1, 0,
                                8, 1, 64, 0.0, 1, 0, 2, None, 0, None, None)
     assert rc == -1 and b"power of two" in L.pkv_last_error()
-    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 0,
+    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 1, 0,
                                8, 1, 60, 0.0, 1, 0, 2, None, 0, None, None)
     assert rc == -1 and b"multiple of 8" in L.pkv_last_error()
-    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 0,
+    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 1, 0,
                                6, 4, 64, 0.0, 1, 0, 2, None, 0, None, None)
     assert rc == -1 and b"multiple of Hkv" in L.pkv_last_error()
-    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 0,
+    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 1, 0,
                                8, 1, 264, 0.0, 1, 0, 2, None, 0, None, None)
     assert rc == -2
     # q_len > 1 needs query_start_loc
-    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 4, 0,
+    rc = L.pkv_paged_attention(1, None, 1, 1, 1, 10, 16, 1, 1, 1, None, 1, 1, 4, 0,
                                8, 1, 64, 0.0, 1, 0, 2, None, 0, None, None)
     assert rc == -1 and b"query_start_loc" in L.pkv_last_error()
     rc = L.pkv_append(1, 1, 10, 1, 1, 1, 5, 64, 7, None, None)

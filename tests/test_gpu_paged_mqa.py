@@ -123,4 +123,7 @@ def test_batched_ragged_step_matches_per_sequence():
         parts = [mqa.forward_paged(x[qsl[i]:qsl[i + 1]][None], pool_b, 0, s.block_table, 0)[0]
                  for i, s in enumerate(seqs)]
     torch.testing.assert_close(out, torch.cat(parts), rtol=0, atol=1e-6)
-    assert torch.equal(pool_a.kv, pool_b.kv)
+    # K/V come from projections of differently sized batches, which round
+    # differently in the last bit; the rows must land in the same slots
+    torch.testing.assert_close(pool_a.kv, pool_b.kv, rtol=0, atol=1e-6)
+    assert torch.equal(pool_a.kv != 0, pool_b.kv != 0)

@@ -37,42 +37,6 @@ __device__ __forceinline__ T from_f32(float x) {
   return (T)x;
 }
 
-__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
-
-// Per-(sequence, kv head, row tile) geometry shared by the attention and
-// merge kernels; both must derive the same partition count.
-struct TileGeom {
-  int q_begin, q_len, rows_here, kv_len, ctx, kv_limit, part_len, nparts;
-};
-
-__device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
-                                          int rows_per_tile, TileGeom& g) {
-  g.q_begin = a.qloc ? a.qloc[s] : s;
-  g.q_len = a.qloc ? a.qloc[s + 1] - g.q_begin : 1;
-  const int rows_total = g.q_len * a.group;
-  const int r0 = tile * rows_per_tile;
-  if (g.q_len <= 0 || r0 >= rows_total) return false;
-  g.rows_here = min(rows_per_tile, rows_total - r0);
-  int kv_len = a.seq_lens[s];
-  const int cap = a.max_blk << a.bs_shift;
-  kv_len = kv_len < cap ? kv_len : cap;
-  g.kv_len = kv_len > 0 ? kv_len : 0;
-  g.ctx = a.causal ? max(g.kv_len - g.q_len, 0) : 0;
-  g.kv_limit = g.kv_len;
-  if (a.causal) {
-    const int i_last = (r0 + g.rows_here - 1) / a.group;
-    g.kv_limit = min(g.kv_limit, g.ctx + i_last + 1);
-  }
-  // A sequence longer than the planned bound still gets every key: its
-  // partitions grow so that their count never exceeds the grid.
-  int plen = a.part_tokens;
-  if (ceil_div(g.kv_limit, plen) > a.parts_max)
-    plen = ceil_div(ceil_div(g.kv_limit, a.parts_max), kChunk) * kChunk;
-  g.part_len = plen;
-  g.nparts = max(1, ceil_div(g.kv_limit, plen));
-  return true;
-}
-
 // ---------------------------------------------------------------------------
 // Generic kernel: any dtype, any group size, any q_len, d <= DMAX.
 // 256 threads; thread t owns row t/8 and, within it, keys (t%8)+8e of each
@@ -90,11 +54,13 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(AttnArgs a) {
   __shared__ float Vs[C][DP];
   __shared__ float Ps[R][C + 1];
 
+  // sequence fastest: consecutive workgroups (round-robin over the XCDs)
+  // belong to different sequences, so every XCD sees a share of the work
   const int tid = threadIdx.x;
-  const int part = blockIdx.x;
+  const int part = blockIdx.z;
   const int tile = blockIdx.y;
-  const int s = blockIdx.z / a.hkv;
-  const int kvh = blockIdx.z - s * a.hkv;
+  const int s = blockIdx.x / a.hkv;
+  const int kvh = blockIdx.x - s * a.hkv;
   TileGeom g;
   if (!tile_geom(a, s, tile, R, g)) return;
   if (part >= g.nparts) return;
@@ -215,7 +181,7 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(AttnArgs a) {
     if (a.lse && c8 == 0) a.lse[qrow] = l > 0.f ? (m + log2f(l)) * kLn2 : INFINITY;
   } else {
     const int64_t unit =
-        ((int64_t)blockIdx.z * a.tiles_max + tile) * a.parts_max + part;
+        ((int64_t)blockIdx.x * a.tiles_max + tile) * a.parts_max + part;
     float* __restrict__ wo = a.ws_o + (unit * R + r) * D;
 #pragma unroll
     for (int jd = 0; jd < NJ; ++jd) {
@@ -233,59 +199,68 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(AttnArgs a) {
 // Split-K merge: for every row of a tile that was split, combine the
 // partitions' (m_p, l_p, o_p): M = max m_p, w_p = 2^(m_p - M),
 // out = sum w_p o_p / sum w_p l_p, lse = (M + log2 sum w_p l_p) ln 2.
-// Grid (tiles, n_seq * hkv); thread t owns row t / 8, columns (t%8) + 8j.
+// Grid (n_seq * hkv, tiles, ceil(rows * d/4 / 256)); one thread per
+// (row, 4 output columns).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a,
                                                          int rows_per_tile) {
-  const int tile = blockIdx.x;
-  const int s = blockIdx.y / a.hkv;
-  const int kvh = blockIdx.y - s * a.hkv;
+  const int tile = blockIdx.y;
+  const int s = blockIdx.x / a.hkv;
+  const int kvh = blockIdx.x - s * a.hkv;
   TileGeom g;
   if (!tile_geom(a, s, tile, rows_per_tile, g)) return;
   if (g.nparts == 1) return;
   const int D = a.d;
+  const int quads = D / 4;
+  const int item = blockIdx.z * kThreads + threadIdx.x;
+  const int r = item / quads;
+  if (r >= g.rows_here) return;
+  const int d0 = (item - r * quads) * 4;
   const int G = a.group;
-  const int r0 = tile * rows_per_tile;
-  const int64_t unit0 = ((int64_t)blockIdx.y * a.tiles_max + tile) * a.parts_max;
-  T* __restrict__ out = static_cast<T*>(a.out);
-  const int lanes_per_row = kThreads / rows_per_tile;
-  for (int r = threadIdx.x / lanes_per_row; r < g.rows_here;
-       r += kThreads / lanes_per_row) {
-    const int c = threadIdx.x % lanes_per_row;
-    float M = -INFINITY;
-    for (int p = 0; p < g.nparts; ++p)
-      M = fmaxf(M, a.ws_ml[((unit0 + p) * rows_per_tile + r) * 2]);
-    const int rg = r0 + r;
-    const int i = rg / G;
-    const int h = rg - i * G;
-    const int64_t qrow = (int64_t)(g.q_begin + i) * a.hq + kvh * G + h;
-    if (M == -INFINITY) {
-      for (int dd = c; dd < D; dd += lanes_per_row) out[qrow * D + dd] = from_f32<T>(0.f);
-      if (a.lse && c == 0) a.lse[qrow] = INFINITY;
-      continue;
-    }
-    float L = 0.f;
+  const int rg = tile * rows_per_tile + r;
+  const int i = rg / G;
+  const int h = rg - i * G;
+  const int64_t qrow = (int64_t)(g.q_begin + i) * a.hq + kvh * G + h;
+  const int64_t unit0 = ((int64_t)blockIdx.x * a.tiles_max + tile) * a.parts_max;
+  T* __restrict__ out = static_cast<T*>(a.out) + qrow * D + d0;
+  float M = -INFINITY;
+  for (int p = 0; p < g.nparts; ++p)
+    M = fmaxf(M, a.ws_ml[((unit0 + p) * rows_per_tile + r) * 2]);
+  float L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (M != -INFINITY) {
     for (int p = 0; p < g.nparts; ++p) {
-      const float* ml = a.ws_ml + ((unit0 + p) * rows_per_tile + r) * 2;
-      L += ml[1] * exp2f(ml[0] - M);
+      const int64_t row = (unit0 + p) * rows_per_tile + r;
+      const float wt = exp2f(a.ws_ml[row * 2] - M);
+      L = fmaf(a.ws_ml[row * 2 + 1], wt, L);
+      const float4 o = *reinterpret_cast<const float4*>(a.ws_o + row * D + d0);
+      acc.x = fmaf(o.x, wt, acc.x);
+      acc.y = fmaf(o.y, wt, acc.y);
+      acc.z = fmaf(o.z, wt, acc.z);
+      acc.w = fmaf(o.w, wt, acc.w);
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    for (int dd = c; dd < D; dd += lanes_per_row) {
-      float acc = 0.f;
-      for (int p = 0; p < g.nparts; ++p) {
-        const int64_t row = (unit0 + p) * rows_per_tile + r;
-        acc = fmaf(a.ws_o[row * D + dd], exp2f(a.ws_ml[row * 2] - M), acc);
-      }
-      out[qrow * D + dd] = from_f32<T>(acc * inv);
-    }
-    if (a.lse && c == 0) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2 : INFINITY;
   }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  out[0] = from_f32<T>(acc.x * inv);
+  out[1] = from_f32<T>(acc.y * inv);
+  out[2] = from_f32<T>(acc.z * inv);
+  out[3] = from_f32<T>(acc.w * inv);
+  if (a.lse && d0 == 0) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2 : INFINITY;
+}
+
+template <typename T>
+int launch_merge(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
+  const int items = p.rows * (a.d / 4);
+  hipLaunchKernelGGL((merge_kernel<T>),
+                     dim3(a.n_seq * a.hkv, p.tiles_max, (items + kThreads - 1) / kThreads),
+                     dim3(kThreads), 0, stream, a, p.rows);
+  return check_launch("merge_kernel");
 }
 
 template <typename T>
 int launch_generic(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
-  const dim3 grid(p.parts_max, p.tiles_max, a.n_seq * a.hkv);
+  const dim3 grid(a.n_seq * a.hkv, p.tiles_max, p.parts_max);
   if (a.d <= 64) {
     hipLaunchKernelGGL((attn_rows_kernel<T, 64>), grid, dim3(kThreads), 0, stream, a);
   } else if (a.d <= 128) {
@@ -295,9 +270,14 @@ int launch_generic(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
   }
   int rc = check_launch("attn_rows_kernel");
   if (rc != PKV_OK || p.parts_max == 1) return rc;
-  hipLaunchKernelGGL((merge_kernel<T>), dim3(p.tiles_max, a.n_seq * a.hkv),
-                     dim3(kThreads), 0, stream, a, p.rows);
-  return check_launch("merge_kernel");
+  return launch_merge<T>(a, p, stream);
+}
+
+template <typename T>
+int launch_mfma(const AttnArgs& a, const AttnPlan& p, int dtype, hipStream_t stream) {
+  int rc = launch_decode_mfma(a, p, dtype, stream);
+  if (rc != PKV_OK || p.parts_max == 1) return rc;
+  return launch_merge<T>(a, p, stream);
 }
 
 int ceil_div_h(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
@@ -307,11 +287,11 @@ int ceil_div_h(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,
                         int part_tokens, int dtype) {
-  (void)dtype;
   AttnPlan p{};
   const int group = hq / hkv;
-  p.kind = 0;
-  p.rows = kGenRows;
+  const bool mfma = decode_mfma_supported(dtype, max_q_len, group, d);
+  p.kind = mfma ? 1 : 0;
+  p.rows = mfma ? group : kGenRows;
   p.tiles_max = ceil_div_h((int64_t)max_q_len * group, p.rows);
   if (p.tiles_max < 1) p.tiles_max = 1;
   const int64_t cap = (int64_t)max_blk * block_size;
@@ -319,7 +299,12 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   if (kvb < 1) kvb = 1;
   const int64_t units = (int64_t)n_seq * hkv * p.tiles_max;
   int plen = part_tokens;
-  if (plen <= 0) {
+  if (plen <= 0 && mfma) {
+    // 4 wavefronts x 2 chunks of 32 tokens each: long enough to pipeline the
+    // loads, short enough that a batch of ordinary contexts splits into
+    // several workgroups per CU
+    plen = 256;
+  } else if (plen <= 0) {
     // Aim for ~2048 workgroups so the 256 CUs stay busy even when most
     // sequences are far below the bound.
     int64_t parts_target = (2048 + units - 1) / (units > 0 ? units : 1);
@@ -340,10 +325,13 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
 int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
                      hipStream_t stream) {
   if (a.n_seq == 0) return PKV_OK;
-  if (p.parts_max > 65535 || p.tiles_max > 65535 ||
-      (int64_t)a.n_seq * a.hkv > 65535)
+  if (p.parts_max > 65535 || p.tiles_max > 65535)
     return fail(PKV_ERR_UNSUPPORTED, "attention grid too large (%d parts, %d tiles, %d seq*hkv)",
                 p.parts_max, p.tiles_max, a.n_seq * a.hkv);
+  if (p.kind == 1) {
+    if (dtype == PKV_DTYPE_BF16) return launch_mfma<bf16>(a, p, dtype, stream);
+    return launch_mfma<f16>(a, p, dtype, stream);
+  }
   switch (dtype) {
     case PKV_DTYPE_F32: return launch_generic<float>(a, p, stream);
     case PKV_DTYPE_F16: return launch_generic<f16>(a, p, stream);

@@ -135,7 +135,8 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
                         const int32_t* block_tables, int max_blk,
                         const int32_t* seq_lens,
                         const int32_t* query_start_loc, int n_seq,
-                        int max_q_len, int max_kv_len, int hq, int hkv, int d,
+                        int n_tokens, int max_q_len, int max_kv_len, int hq,
+                        int hkv, int d,
                         float scale, int causal, int part_tokens, int dtype,
                         void* workspace, size_t workspace_bytes, int* status,
                         void* stream) {
@@ -149,9 +150,12 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
   const int bs_shift = log2_exact(block_size);
   if (bs_shift < 0)
     return fail(PKV_ERR_INVALID, "blocksize %d must be a power of two", block_size);
-  if (n_seq < 0 || max_blk < 0 || num_blocks < 0 || max_q_len < 0)
+  if (n_seq < 0 || max_blk < 0 || num_blocks < 0 || max_q_len < 0 || n_tokens < 0)
     return fail(PKV_ERR_INVALID, "bad sizes");
-  if (n_seq == 0 || max_q_len == 0) return PKV_OK;
+  if (!query_start_loc && n_tokens != n_seq)
+    return fail(PKV_ERR_INVALID, "without query_start_loc, n_tokens (%d) must equal n_seq (%d)",
+                n_tokens, n_seq);
+  if (n_seq == 0 || max_q_len == 0 || n_tokens == 0) return PKV_OK;
   if (!out || !q || !k_pool || !v_pool || !seq_lens || (max_blk > 0 && !block_tables))
     return fail(PKV_ERR_INVALID, "null pointer argument");
   if (!query_start_loc && max_q_len != 1)
@@ -176,6 +180,7 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
   a.bs_shift = bs_shift;
   a.max_blk = max_blk;
   a.n_seq = n_seq;
+  a.n_tokens = n_tokens;
   a.hq = hq;
   a.hkv = hkv;
   a.group = hq / hkv;

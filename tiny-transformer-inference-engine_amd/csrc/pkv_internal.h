@@ -60,6 +60,7 @@ struct AttnArgs {
   int bs_shift;
   int max_blk;
   int n_seq;
+  int n_tokens;  // T: rows of q / out
   int hq;
   int hkv;
   int group;  // hq / hkv
@@ -88,11 +89,60 @@ struct AttnPlan {
   size_t ws_bytes;
 };
 
+// Per-(sequence, kv head, row tile) geometry shared by every attention kernel
+// and the split-K merge; all of them must derive the same partition count.
+__device__ __forceinline__ int dceil_div(int a, int b) { return (a + b - 1) / b; }
+
+struct TileGeom {
+  int q_begin, q_len, rows_here, kv_len, ctx, kv_limit, part_len, nparts;
+};
+
+__device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
+                                          int rows_per_tile, TileGeom& g) {
+  g.q_begin = a.qloc ? a.qloc[s] : s;
+  g.q_len = a.qloc ? a.qloc[s + 1] - g.q_begin : 1;
+  if (g.q_len <= 0) return false;
+  if (g.q_begin < 0 || g.q_begin + g.q_len > a.n_tokens) {
+    // malformed query_start_loc: never index q / out outside [0, T)
+    if (a.status && tile == 0) atomicOr(a.status, PKV_STATUS_BAD_QLOC);
+    return false;
+  }
+  const int rows_total = g.q_len * a.group;
+  const int r0 = tile * rows_per_tile;
+  if (r0 >= rows_total) return false;
+  g.rows_here = min(rows_per_tile, rows_total - r0);
+  int kv_len = a.seq_lens[s];
+  const int cap = a.max_blk << a.bs_shift;
+  kv_len = kv_len < cap ? kv_len : cap;
+  g.kv_len = kv_len > 0 ? kv_len : 0;
+  g.ctx = a.causal ? max(g.kv_len - g.q_len, 0) : 0;
+  g.kv_limit = g.kv_len;
+  if (a.causal) {
+    const int i_last = (r0 + g.rows_here - 1) / a.group;
+    g.kv_limit = min(g.kv_limit, g.ctx + i_last + 1);
+  }
+  // A sequence longer than the planned bound still gets every key: its
+  // partitions grow so that their count never exceeds the grid.
+  int plen = a.part_tokens;
+  if (dceil_div(g.kv_limit, plen) > a.parts_max)
+    plen = dceil_div(dceil_div(g.kv_limit, a.parts_max), kChunk) * kChunk;
+  g.part_len = plen;
+  g.nparts = max(1, dceil_div(g.kv_limit, plen));
+  return true;
+}
+
+
 AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,
                         int part_tokens, int dtype);
 
 int launch_attention(const AttnArgs& a, const AttnPlan& plan, int dtype,
                      hipStream_t stream);
+
+// MFMA decode kernel (decode_mfma.hip): bf16/fp16, one query per sequence,
+// group 16 or 32, head dim 64 or 128.
+bool decode_mfma_supported(int dtype, int max_q_len, int group, int d);
+int launch_decode_mfma(const AttnArgs& a, const AttnPlan& plan, int dtype,
+                       hipStream_t stream);
 
 }  // namespace pkv

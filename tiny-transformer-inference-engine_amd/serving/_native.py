@@ -20,6 +20,7 @@ DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 PKV_STATUS_BAD_SLOT = 1
 PKV_STATUS_BAD_BLOCK = 2
 PKV_STATUS_SHORT_TABLE = 4
+PKV_STATUS_BAD_QLOC = 8
 
 _lib = None
 _lock = threading.Lock()
@@ -44,7 +45,7 @@ _SIGNATURES = {
                                        _c_int, _c_int, _c_int, _c_int, _c_int],
                                       _c_size),
     "pkv_paged_attention": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int,
-                             _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int,
+                             _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int,
                              _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
                              _c_int, _c_int, _c_vp, _c_size, _c_vp, _c_vp],
                             _c_int),

@@ -65,7 +65,7 @@ def _launch(q, k_pool, v_pool, block_tables, seq_lens, queryloc, n_seq,
     rc = L.pkv_paged_attention(
         out.data_ptr(), _native.ptr(lse), q.data_ptr(), k_pool.data_ptr(),
         v_pool.data_ptr(), nb, bs, block_tables.data_ptr() if max_blk else None,
-        max_blk, seq_lens.data_ptr(), _native.ptr(queryloc), n_seq, max_q_len,
+        max_blk, seq_lens.data_ptr(), _native.ptr(queryloc), n_seq, T, max_q_len,
         max_kv_len, hq, hkv, d, float(scale), int(bool(causal)), part_tokens,
         code, _native.ptr(ws), ws_bytes, None, _native.stream_ptr(q.device))
     _native.check(rc, "pkv_paged_attention")
