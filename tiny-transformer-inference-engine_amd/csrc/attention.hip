@@ -300,10 +300,10 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   const int64_t units = (int64_t)n_seq * hkv * p.tiles_max;
   int plen = part_tokens;
   if (plen <= 0 && mfma) {
-    // 4 wavefronts x 2 chunks of 32 tokens each: long enough to pipeline the
-    // loads, short enough that a batch of ordinary contexts splits into
-    // several workgroups per CU
-    plen = 256;
+    // 4 wavefronts x 4 chunks of 32 tokens: long enough to amortise the
+    // workgroup prologue (table slice, Q) and keep loads pipelined, short
+    // enough that ordinary contexts split into several workgroups
+    plen = 512;
   } else if (plen <= 0) {
     // Aim for ~2048 workgroups so the 256 CUs stay busy even when most
     // sequences are far below the bound.
