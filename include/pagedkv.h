@@ -47,6 +47,11 @@ extern "C" {
 #define PKV_DTYPE_F16 1
 #define PKV_DTYPE_BF16 2
 
+/* part_tokens value of pkv_paged_attention selecting the persistent
+   (stream-K) decode kernel where it applies (bf16/f16, one query per
+   sequence, 16 or 32 query heads per kv head, d = 64 or 128). */
+#define PKV_PART_PERSISTENT (-1)
+
 #define PKV_OK 0
 #define PKV_ERR_INVALID (-1)     /* bad argument (shape, null pointer, ...) */
 #define PKV_ERR_UNSUPPORTED (-2) /* valid but unsupported configuration   */
@@ -111,6 +116,9 @@ int pkv_gather(void* k_out, void* v_out, const void* k_pool,
 /*
  * Bytes of workspace pkv_paged_attention needs for this problem (0 when no
  * sequence is split). `max_kv_len` <= 0 means max_blk * block_size.
+ * The first 256 KiB of a workspace are arrival counters of the persistent
+ * decode kernel: they must be zero before the workspace is first used, and
+ * every call leaves them zero. Calls that overlap on one workspace race.
  */
 size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
                                      int d, int max_blk, int block_size,
@@ -134,8 +142,10 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
  * h / (hq / hkv). scale <= 0 means 1/sqrt(d). Rows with no visible key give
  * out = 0 and lse = +inf. lse = m + ln(l) in natural-log units.
  * `max_q_len` must bound every q_len; `max_kv_len` (<= 0: the table
- * capacity) must bound every kv_len; `part_tokens` (0: automatic) is the
- * split-K partition length. Workspace: pkv_attention_workspace_bytes().
+ * capacity) must bound every kv_len; `part_tokens` is the split-K
+ * partition length (0: automatic; PKV_PART_PERSISTENT: one persistent
+ * workgroup per CU slot, each taking an equal share of all context chunks).
+ * Workspace: pkv_attention_workspace_bytes().
  */
 int pkv_paged_attention(void* out, float* lse, const void* q,
                         const void* k_pool, const void* v_pool,

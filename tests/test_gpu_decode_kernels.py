@@ -1,0 +1,126 @@
+"""The two MFMA decode kernels (the split-K partition form, the default, and
+the persistent stream-K form selected by part_tokens = PART_PERSISTENT)
+against the fp64 oracle, on the shapes that stress their work decomposition:
+
+  - one very long sequence, cut by every workgroup share (all partials,
+    one last-arriving merger);
+  - hundreds of short sequences, many inside one share (finished in place);
+  - empty contexts (kv_len = 0 -> zero row, lse = +inf) mixed with others;
+  - sequences with no query this step (query_start_loc with q_len 0);
+  - repeated calls on one workspace (the arrival counters must reset), and
+    the counter region must be all zero after every call.
+bf16/fp16 tolerance 2e-2 absolute (bf16 P in the PV product).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_ref as ref
+from serving import _native, workloads
+from serving.fake_paged_attn import paged_attn_fwd, paged_mqa_decode
+
+pytestmark = pytest.mark.gpu
+SK = _native.PART_PERSISTENT
+DEV = "cuda"
+SHAPES = [(16, 64), (32, 128), (16, 128), (32, 64)]  # (heads per kv head, D)
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def oracle(p, lens=None, qsl=None):
+    lens = p.seq_lens if lens is None else lens
+    return ref.paged_attention(np64(p.q), np64(p.k_pool), np64(p.v_pool),
+                               p.block_tables.cpu().numpy(), lens.cpu().numpy(),
+                               None if qsl is None else qsl.cpu().numpy())
+
+
+def check(out, lse, eo, el, what):
+    got = np64(out)
+    assert np.all(np.isfinite(got)), what
+    err = np.abs(got - eo).max()
+    assert err <= 2e-2, f"{what}: max err {err:.3e}"
+    if lse is not None:
+        L = lse.cpu().numpy()
+        fin = np.isfinite(el)
+        assert np.array_equal(np.isinf(L), ~fin), f"{what}: lse infinities"
+        np.testing.assert_allclose(L[fin], el[fin], rtol=0, atol=2e-2, err_msg=what)
+
+
+def counters_zero():
+    for buf in _native.WORKSPACE._bufs.values():
+        assert not buf[: 256 * 1024].any(), "arrival counters not left at zero"
+
+
+@pytest.mark.parametrize("g,d", SHAPES)
+@pytest.mark.parametrize("part_tokens", [SK, 0, 512])
+def test_single_long_sequence(g, d, part_tokens):
+    print(f"[decode long] g={g} d={d} part={part_tokens}", flush=True)
+    p = workloads.decode_problem([30000], g, 1, d, 16, 2048, torch.bfloat16, DEV, seed=11)
+    lse = torch.empty(1, g, device=DEV)
+    out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, lse=lse,
+                           part_tokens=part_tokens)
+    torch.cuda.synchronize()
+    eo, el = oracle(p)
+    check(out, lse, eo, el, "long")
+    counters_zero()
+
+
+@pytest.mark.parametrize("g,d", SHAPES)
+def test_many_short_and_empty_sequences_repeated(g, d):
+    print(f"[decode short] g={g} d={d}", flush=True)
+    rng = np.random.default_rng(12)
+    lens = rng.integers(1, 90, size=600)
+    lens[::17] = 0      # empty contexts
+    lens[5] = 4000      # one long one among them
+    p = workloads.decode_problem(np.maximum(lens, 1), g, 1, d, 16, 8192, torch.bfloat16,
+                                 DEV, seed=12)
+    seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
+    eo, el = oracle(p, seq_lens)
+    for rep in range(3):
+        lse = torch.empty(len(lens), g, device=DEV)
+        out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
+                               part_tokens=SK)
+        torch.cuda.synchronize()
+        check(out, lse, eo, el, f"short rep {rep}")
+        counters_zero()
+    # the partition kernel agrees
+    out2 = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, part_tokens=256)
+    check(out2, None, eo, el, "partition kernel")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gqa_two_kv_heads_and_missing_queries(dtype):
+    # hkv = 2 (32 query heads), query_start_loc with empty query ranges
+    g, d, hkv = 16, 128, 2
+    lens = [700, 3, 1500, 64, 1]
+    p = workloads.decode_problem(lens, g * hkv, hkv, d, 32, 512, dtype, DEV, seed=13)
+    qlens = [1, 0, 1, 1, 0]
+    qsl = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device=DEV)
+    T = int(sum(qlens))
+    q = p.q[:T].contiguous()
+    eo, el = ref.paged_attention(np64(q), np64(p.k_pool), np64(p.v_pool),
+                                 p.block_tables.cpu().numpy(), p.seq_lens.cpu().numpy(),
+                                 qsl.cpu().numpy())
+    for pt in (0, SK):
+        O = torch.empty_like(q)
+        L = torch.empty(T, g * hkv, device=DEV)
+        paged_mqa_decode(q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, out=O, lse=L,
+                         query_start_loc=qsl, part_tokens=pt)
+        torch.cuda.synchronize()
+        check(O, L, eo, el, f"gqa part_tokens={pt}")
+        counters_zero()
+
+
+def test_cfg4_and_cfg5_kernels_agree():
+    for name, p in [("cfg4", workloads.cfg4_problem(DEV)), ("cfg5", workloads.cfg5_problem(DEV))]:
+        mk = int(p.lens.max())
+        a = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
+                             part_tokens=SK)
+        b = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
+                             part_tokens=512)
+        torch.cuda.synchronize()
+        diff = (a.float() - b.float()).abs().max().item()
+        assert diff <= 2e-2, f"{name}: persistent vs partition kernel differ by {diff}"
+        counters_zero()

@@ -290,6 +290,18 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   AttnPlan p{};
   const int group = hq / hkv;
   const bool mfma = decode_mfma_supported(dtype, max_q_len, group, d);
+  const int64_t virt = (int64_t)n_seq * hkv;
+  if (mfma && part_tokens == PKV_PART_PERSISTENT && virt <= kMaxCounters) {
+    // persistent kernel: partials of at most two segments per workgroup
+    p.kind = 2;
+    p.rows = group;
+    p.tiles_max = 1;
+    p.part_tokens = 0;
+    p.parts_max = 1;
+    p.ws_bytes = kWsCounterBytes +
+                 (size_t)kSkMaxWg * 2 * group * ((size_t)d + 2) * sizeof(float);
+    return p;
+  }
   p.kind = mfma ? 1 : 0;
   p.rows = mfma ? group : kGenRows;
   p.tiles_max = ceil_div_h((int64_t)max_q_len * group, p.rows);
@@ -300,10 +312,12 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   const int64_t units = (int64_t)n_seq * hkv * p.tiles_max;
   int plen = part_tokens;
   if (plen <= 0 && mfma) {
-    // 4 wavefronts x 4 chunks of 32 tokens: long enough to amortise the
-    // workgroup prologue (table slice, Q) and keep loads pipelined, short
-    // enough that ordinary contexts split into several workgroups
+    // at least 4 wavefronts x 4 chunks of 32 tokens, to amortise the
+    // workgroup prologue (table slice, Q) and keep loads pipelined; longer
+    // bounds get longer partitions so the longest context splits into at
+    // most 8 partials (merge work and partial traffic stay bounded)
     plen = 512;
+    while (plen < 4096 && (int64_t)plen * 8 < kvb) plen *= 2;
   } else if (plen <= 0) {
     // Aim for ~2048 workgroups so the 256 CUs stay busy even when most
     // sequences are far below the bound.
@@ -317,9 +331,24 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   p.parts_max = ceil_div_h(kvb, plen);
   if (p.parts_max < 1) p.parts_max = 1;
   p.ws_bytes = p.parts_max > 1
-                   ? (size_t)units * p.parts_max * p.rows * ((size_t)d + 2) * sizeof(float)
+                   ? kWsCounterBytes + (size_t)units * p.parts_max * p.rows *
+                                           ((size_t)d + 2) * sizeof(float)
                    : 0;
   return p;
+}
+
+int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
 }
 
 int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
@@ -328,6 +357,15 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
   if (p.parts_max > 65535 || p.tiles_max > 65535)
     return fail(PKV_ERR_UNSUPPORTED, "attention grid too large (%d parts, %d tiles, %d seq*hkv)",
                 p.parts_max, p.tiles_max, a.n_seq * a.hkv);
+  if (p.kind == 2) {
+    SkArgs k{};
+    k.n_wg = 2 * device_cu_count() < kSkMaxWg ? 2 * device_cu_count() : kSkMaxWg;
+    char* ws = reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes;
+    k.counters = reinterpret_cast<int*>(ws);
+    k.part_o = a.ws_o;
+    k.part_ml = a.ws_o + (size_t)kSkMaxWg * 2 * a.group * a.d;
+    return launch_decode_sk(a, k, dtype, stream);
+  }
   if (p.kind == 1) {
     if (dtype == PKV_DTYPE_BF16) return launch_mfma<bf16>(a, p, dtype, stream);
     return launch_mfma<f16>(a, p, dtype, stream);

@@ -190,10 +190,13 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
   a.part_tokens = plan.part_tokens;
   a.parts_max = plan.parts_max;
   a.tiles_max = plan.tiles_max;
-  float* ws = static_cast<float*>(workspace);
+  // partials live after the counter region (see kWsCounterBytes)
+  float* ws = plan.ws_bytes
+                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kWsCounterBytes)
+                  : nullptr;
   const size_t units = (size_t)n_seq * hkv * plan.tiles_max * plan.parts_max;
-  a.ws_o = plan.ws_bytes ? ws : nullptr;
-  a.ws_ml = plan.ws_bytes ? ws + units * plan.rows * (size_t)d : nullptr;
+  a.ws_o = ws;
+  a.ws_ml = ws ? ws + units * plan.rows * (size_t)d : nullptr;
   a.status = status;
   return launch_attention(a, plan, dtype, (hipStream_t)stream);
 }

@@ -1,0 +1,303 @@
+// Building blocks shared by the gfx950 MFMA decode kernels (decode_mfma.hip:
+// one workgroup per context partition; decode_sk.hip: persistent workgroups
+// over equal shares of all sequences' chunks).
+//
+// A wavefront processes the context in 32-token chunks. Per chunk it
+//   1. stores the chunk's K and V rows, prefetched into registers by 16-byte
+//      coalesced loads through the block table, into its private LDS slice
+//      (rows padded so the fragment reads below are bank-conflict free);
+//   2. issues the loads of the chunk it will process PF chunks later;
+//   3. computes S^T = K Q^T with v_mfma_f32_16x16x32 (A = 16 tokens x 32 dims
+//      from LDS, B = Q^T in registers), so each K row is read once for all
+//      heads of the group;
+//   4. updates the online softmax per head in base 2 (each lane owns one head
+//      and 8 of the 32 tokens; the row max is a 4-lane xor shuffle);
+//   5. computes O^T += V^T P^T with the same instruction: the S^T accumulator
+//      layout already is the P^T operand layout (lane = head, 8 tokens), and
+//      V^T fragments are gathered from LDS with 16-bit reads.
+//
+// MFMA operand layouts relied upon (16x16x32, wave64): lane l supplies row
+// l%16 of A and column l%16 of B, each with the 8 k-values of group l/16 (the
+// k order inside a group is the same for A and B, which is all a reduction
+// needs); lane l receives D[4*(l/16) + r][l%16] for r = 0..3.
+#pragma once
+
+#include "pkv_internal.h"
+
+namespace pkv {
+namespace mfma {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Ops;
+template <>
+struct Ops<bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ floatx4 mma(v8 a, v8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Ops<f16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ floatx4 mma(v8 a, v8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kTblCap = 256;  // block-table entries staged in LDS at a time
+constexpr float kLn2f = 0.6931471805599453f;
+
+// LDS geometry of one 32-token chunk of K (or V) rows, D bf16/fp16 each.
+// Rows are padded by 16 bytes (PITCH = 2D + 16): row r starts 4r (mod 64)
+// banks further on for D = 128 (36r for D = 64), so the 16 rows an MFMA
+// fragment read touches at one 16-byte piece land on distinct bank groups,
+// and so do the 4 row groups of a V^T gather. Every fragment address is then
+// one base register plus an immediate offset.
+template <int D>
+struct ChunkGeo {
+  static constexpr int CPR = D / 8;                 // 16-byte pieces per row
+  static constexpr int ROW_BYTES = D * 2;
+  static constexpr int PITCH = ROW_BYTES + 16;
+  static constexpr int ROWS_PER_LOAD = 64 / CPR;    // rows one wave load covers
+  static constexpr int NPL = kChunk / ROWS_PER_LOAD;  // loads per lane per tensor
+  static constexpr int BYTES = kChunk * PITCH;
+  static_assert(ROWS_PER_LOAD >= 1 && 64 % CPR == 0, "D must be 64 or 128");
+  static __device__ __forceinline__ int off(int r, int c) { return r * PITCH + (c << 4); }
+};
+
+// K and V rows of one 32-token chunk held in registers between their loads
+// and their LDS stores; bit j of `valid` clears row load j (bad table entry).
+template <int NPL>
+struct ChunkRegs {
+  u32x4 k[NPL];
+  u32x4 v[NPL];
+  unsigned valid;
+};
+
+// Pool addressing shared by all chunks of a wavefront.
+struct PoolView {
+  const char* kbase;
+  const char* vbase;
+  int64_t row_stride;  // bytes per pool slot (hkv * d * 2)
+  int64_t head_off;    // byte offset of this kv head inside a slot
+  int num_blocks;
+  int bs_shift;
+};
+
+// Where a wavefront is in the current run of chunks: its LDS slices, the
+// block-table window staged in LDS, and the token range [seg_lo, seg_hi).
+struct ChunkCtx {
+  char* kl;
+  char* vl;
+  const int* tbl;
+  int blk_lo;
+  int seg_lo;
+  int seg_hi;
+  int prow;  // first row this lane loads
+  int pcol;  // its 16-byte piece within the row
+  int grp;   // MFMA k-group of this lane (lane / 16)
+  int l16;   // lane % 16
+  float scale_log2;
+};
+
+// Branch-free loads of chunk `c` (tokens seg_lo + 32c ...): rows past
+// seg_hi re-read the range's last row (their scores are masked to -inf, so
+// they contribute exactly 0); rows whose table entry is outside the pool
+// read block 0 and are zeroed when staged. Nothing here consumes a load
+// result, so the loads stay in flight until the chunk is staged.
+// OFF64 = false when every byte offset of the pool fits in 31 bits: the load
+// is then a uniform base plus a 32-bit per-lane offset.
+template <class Geo, int NPL, bool OFF64>
+__device__ __forceinline__ void load_chunk(ChunkRegs<NPL>& r, const PoolView& pv,
+                                           const ChunkCtx& cx, int c) {
+  const int bs_mask = (1 << pv.bs_shift) - 1;
+  const int cb = cx.seg_lo + c * kChunk;
+  unsigned vmask = 0;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    int pos = cb + cx.prow + j * Geo::ROWS_PER_LOAD;
+    pos = pos < cx.seg_hi ? pos : cx.seg_hi - 1;
+    const int phys = cx.tbl[(pos >> pv.bs_shift) - cx.blk_lo];
+    const bool ok = (unsigned)phys < (unsigned)pv.num_blocks;
+    vmask |= (unsigned)ok << j;
+    const int slot = ((ok ? phys : 0) << pv.bs_shift) + (pos & bs_mask);
+    if constexpr (OFF64) {
+      const int64_t off = (int64_t)slot * pv.row_stride + pv.head_off + cx.pcol * 16;
+      r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.kbase + off));
+      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.vbase + off));
+    } else {
+      const unsigned off = (unsigned)slot * (unsigned)pv.row_stride +
+                           (unsigned)pv.head_off + (unsigned)(cx.pcol * 16);
+      r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.kbase + off));
+      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.vbase + off));
+    }
+  }
+  r.valid = vmask;
+}
+
+// Online-softmax state of one wavefront: lane l holds head 16*nt + l%16,
+// output dims 16*dt + 4*(l/16) + 0..3.
+template <int NT, int DT>
+struct WaveState {
+  floatx4 o[NT][DT];
+  float m[NT];
+  float l[NT];
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      m[nt] = -INFINITY;
+      l[nt] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[nt][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+};
+
+// One chunk: registers -> LDS slice, optionally refill the registers with
+// chunk `c + ahead`, then QK / softmax / PV out of LDS.
+template <typename T, int D, int NT, int NPL, bool OFF64>
+__device__ __forceinline__ void chunk_step(
+    ChunkRegs<NPL>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
+    const PoolView& pv, const typename Ops<T>::v8 (&qf)[NT][D / 32],
+    WaveState<NT, D / 16>& st, bool& bad_block) {
+  using Geo = ChunkGeo<D>;
+  using v8 = typename Ops<T>::v8;
+  constexpr int KS = D / 32;
+  constexpr int DT = D / 16;
+  asm volatile("" ::: "memory");
+  const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int row = cx.prow + j * Geo::ROWS_PER_LOAD;
+    const bool ok = (r.valid >> j) & 1;
+    bad_block |= !ok;
+    *reinterpret_cast<u32x4*>(cx.kl + Geo::off(row, cx.pcol)) = ok ? r.k[j] : zero;
+    *reinterpret_cast<u32x4*>(cx.vl + Geo::off(row, cx.pcol)) = ok ? r.v[j] : zero;
+  }
+  if (refill) load_chunk<Geo, NPL, OFF64>(r, pv, cx, c + ahead);
+  // the slice is private to this wavefront: waiting for its own LDS writes
+  // is the only synchronisation the reads below need
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  // S^T = K Q^T, tokens 16h + 4*grp + r of this chunk for head 16nt + l16
+  floatx4 sacc[NT][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v8 kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[ks] = *reinterpret_cast<const v8*>(cx.kl + Geo::off(16 * h + cx.l16, 4 * ks + cx.grp));
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc = Ops<T>::mma(kf[ks], qf[nt][ks], acc);
+      sacc[nt][h] = acc;
+    }
+  }
+
+  // online softmax (base 2); P^T operand = this lane's 8 probabilities
+  const int cb = cx.seg_lo + c * kChunk;
+  v8 pf[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int pos = cb + 16 * h + 4 * cx.grp + rr;
+        const float x = pos < cx.seg_hi ? sacc[nt][h][rr] * cx.scale_log2 : -INFINITY;
+        sv[4 * h + rr] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(st.m[nt], mx);
+    const float ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(st.m[nt] - ref);
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = exp2f(sv[e] - ref);
+      ps += p;
+      pf[nt][e] = (T)p;
+    }
+    st.l[nt] = st.l[nt] * alpha + ps;
+    st.m[nt] = m_new;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.o[nt][dt] *= alpha;
+  }
+
+  // O^T += V^T P^T; V^T fragment: dims 16dt + l16, the same 8 tokens
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    v8 vf;
+    const int d = 16 * dt + cx.l16;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = (e < 4 ? 0 : 16) + 4 * cx.grp + (e & 3);
+      vf[e] = *reinterpret_cast<const T*>(cx.vl + Geo::off(tok, d >> 3) + (d & 7) * 2);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) st.o[nt][dt] = Ops<T>::mma(vf, pf[nt], st.o[nt][dt]);
+  }
+}
+
+// All chunks of [cx.seg_lo, cx.seg_hi) assigned to wavefront w of nw:
+// chunks w, w + nw, ... with PF chunks in flight per wavefront. A
+// steady-state loop with no data-dependent branch keeps the compiler's wait
+// counts exact (staging buffer b waits only for buffer b's loads).
+template <typename T, int D, int NT, int PF, bool OFF64>
+__device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
+                                           const PoolView& pv,
+                                           const typename Ops<T>::v8 (&qf)[NT][D / 32],
+                                           WaveState<NT, D / 16>& st, bool& bad_block) {
+  using Geo = ChunkGeo<D>;
+  constexpr int NPL = Geo::NPL;
+  const int nchunks = (cx.seg_hi - cx.seg_lo + kChunk - 1) / kChunk;
+  const int step = nw * PF;
+  ChunkRegs<NPL> rb[PF];
+#pragma unroll
+  for (int b = 0; b < PF; ++b)
+    if (w + nw * b < nchunks) load_chunk<Geo, NPL, OFF64>(rb[b], pv, cx, w + nw * b);
+  int c = w;
+  for (; c + nw * (2 * PF - 1) < nchunks; c += step) {
+#pragma unroll
+    for (int b = 0; b < PF; ++b)
+      chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, true, step, cx, pv, qf, st,
+                                       bad_block);
+  }
+#pragma unroll
+  for (int b = 0; b < PF; ++b)
+    if (c + nw * b < nchunks)
+      chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, c + nw * (b + PF) < nchunks, step,
+                                       cx, pv, qf, st, bad_block);
+  c += step;
+#pragma unroll
+  for (int b = 0; b < PF; ++b)
+    if (c + nw * b < nchunks)
+      chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, false, step, cx, pv, qf, st,
+                                       bad_block);
+}
+
+// Q^T fragments of one (token, kv head): head 16*nt + l16, dims of piece
+// 4*ks + grp.
+template <typename T, int D, int NT>
+__device__ __forceinline__ void load_q(typename Ops<T>::v8 (&qf)[NT][D / 32], const T* q,
+                                       int64_t qrow0, int grp, int l16) {
+  using v8 = typename Ops<T>::v8;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks)
+      qf[nt][ks] = *reinterpret_cast<const v8*>(q + (qrow0 + 16 * nt + l16) * D +
+                                               (4 * ks + grp) * 8);
+}
+
+}  // namespace mfma
+}  // namespace pkv

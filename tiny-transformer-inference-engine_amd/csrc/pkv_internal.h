@@ -80,8 +80,24 @@ struct AttnArgs {
 constexpr int kGenRows = 32;
 constexpr int kChunk = 32;  // kv tokens staged per iteration
 
+// Workspace layout: the first kWsCounterBytes hold the persistent decode
+// kernel's arrival counters (one int per sequence x kv head). They must be
+// zero before the first call and every call leaves them zero; no other
+// kernel touches them. Partials start after them.
+constexpr size_t kWsCounterBytes = 256 * 1024;
+constexpr int kMaxCounters = (int)(kWsCounterBytes / sizeof(int));
+constexpr int kSkMaxWg = 512;  // workgroups of the persistent kernel, at most
+
+struct SkArgs {
+  int n_wg;         // workgroups launched (one per CU)
+  int* counters;    // [n_seq * hkv] arrival counters
+  float* part_o;    // [n_wg][2][G][D] partial outputs
+  float* part_ml;   // [n_wg][2][G][2] partial (max, sum)
+};
+
 struct AttnPlan {
-  int kind;        // 0 = generic rows kernel, 1 = MFMA decode kernel
+  int kind;        // 0 = generic rows kernel, 1 = MFMA partition kernel,
+                   // 2 = MFMA persistent kernel
   int rows;        // rows per tile of the chosen kernel
   int part_tokens;
   int parts_max;
@@ -142,7 +158,12 @@ int launch_attention(const AttnArgs& a, const AttnPlan& plan, int dtype,
 // MFMA decode kernel (decode_mfma.hip): bf16/fp16, one query per sequence,
 // group 16 or 32, head dim 64 or 128.
 bool decode_mfma_supported(int dtype, int max_q_len, int group, int d);
+bool pool_needs_off64(const AttnArgs& a);
 int launch_decode_mfma(const AttnArgs& a, const AttnPlan& plan, int dtype,
                        hipStream_t stream);
+// Persistent MFMA decode kernel (decode_sk.hip), same coverage.
+int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream);
+// CUs of the current device (cached; 256 when no device is visible).
+int device_cu_count();
 
 }  // namespace pkv

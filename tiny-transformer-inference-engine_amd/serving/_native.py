@@ -21,6 +21,8 @@ PKV_STATUS_BAD_SLOT = 1
 PKV_STATUS_BAD_BLOCK = 2
 PKV_STATUS_SHORT_TABLE = 4
 PKV_STATUS_BAD_QLOC = 8
+# part_tokens value selecting the persistent (stream-K) decode kernel
+PART_PERSISTENT = -1
 
 _lib = None
 _lock = threading.Lock()
@@ -118,9 +120,11 @@ def ptr(t) -> int | None:
 
 
 class Workspace:
-    """Per-device scratch for split-K partials, grown on demand and reused
-    (the library never allocates). Allocation goes through torch's caching
-    allocator, so it is stream-ordered on the current stream."""
+    """Per-device scratch for split-K partials and the persistent kernel's
+    arrival counters, grown on demand and reused (the library never
+    allocates). Allocation goes through torch's caching allocator, so it is
+    stream-ordered on the current stream; calls on other streams need their
+    own Workspace."""
 
     def __init__(self):
         self._bufs: dict[int, torch.Tensor] = {}
@@ -133,7 +137,9 @@ class Workspace:
         if buf is None or buf.numel() < nbytes:
             # grow geometrically so ragged batches do not reallocate every step
             size = max(nbytes, 0 if buf is None else 2 * buf.numel())
-            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            # zeroed: the leading counter region must start at zero (the
+            # kernels leave it zero after every call)
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
             self._bufs[idx] = buf
         return buf
 

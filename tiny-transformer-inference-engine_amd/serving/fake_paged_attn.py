@@ -219,14 +219,20 @@ def paged_mqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
                      scale: Optional[float] = None, max_kv_len: int = 0,
                      out: Optional[torch.Tensor] = None,
                      lse: Optional[torch.Tensor] = None,
-                     part_tokens: int = 0) -> torch.Tensor:
+                     part_tokens: int = 0,
+                     query_start_loc: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One decode query per sequence (q [N, Hq, D]) against device-resident
     int32 block_tables [N, max_blk] and seq_lens [N]. `max_kv_len` (0: table
-    capacity) bounds the context and sizes the split-K grid."""
+    capacity) bounds the context and sizes the split-K grid. With
+    `query_start_loc` (int32 [n_seq + 1], every range 0 or 1 token long) q
+    holds only the sequences that have a query this step. `part_tokens`:
+    0 automatic, > 0 the split-K partition length, _native.PART_PERSISTENT
+    the persistent kernel."""
     _native.require_device(q, k_pool, v_pool, block_tables, seq_lens, what="paged_mqa_decode")
     if out is None:
         out = torch.empty_like(q)
-    _launch(q, k_pool, v_pool, block_tables, seq_lens, None, q.shape[0], 1,
+    n_seq = q.shape[0] if query_start_loc is None else block_tables.shape[0]
+    _launch(q, k_pool, v_pool, block_tables, seq_lens, query_start_loc, n_seq, 1,
             int(max_kv_len), scale if scale is not None and scale > 0 else 0.0,
             True, out, lse, part_tokens)
     return out
