@@ -116,9 +116,8 @@ int pkv_gather(void* k_out, void* v_out, const void* k_pool,
 /*
  * Bytes of workspace pkv_paged_attention needs for this problem (0 when no
  * sequence is split). `max_kv_len` <= 0 means max_blk * block_size.
- * The first 256 KiB of a workspace are arrival counters of the persistent
- * decode kernel: they must be zero before the workspace is first used, and
- * every call leaves them zero. Calls that overlap on one workspace race.
+ * The workspace holds partial results between the kernels of one call and
+ * needs no initialisation. Calls that overlap on one workspace race.
  */
 size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
                                      int d, int max_blk, int block_size,
@@ -143,8 +142,10 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
  * out = 0 and lse = +inf. lse = m + ln(l) in natural-log units.
  * `max_q_len` must bound every q_len; `max_kv_len` (<= 0: the table
  * capacity) must bound every kv_len; `part_tokens` is the split-K
- * partition length (0: automatic; PKV_PART_PERSISTENT: one persistent
- * workgroup per CU slot, each taking an equal share of all context chunks).
+ * partition length (0: automatic, the persistent kernel for context bounds
+ * of 4096 tokens and more where it applies, else fixed partitions;
+ * PKV_PART_PERSISTENT: one persistent workgroup per CU slot, each taking an
+ * equal share of all context chunks).
  * Workspace: pkv_attention_workspace_bytes().
  */
 int pkv_paged_attention(void* out, float* lse, const void* q,

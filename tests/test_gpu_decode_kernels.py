@@ -7,8 +7,8 @@ against the fp64 oracle, on the shapes that stress their work decomposition:
   - hundreds of short sequences, many inside one share (finished in place);
   - empty contexts (kv_len = 0 -> zero row, lse = +inf) mixed with others;
   - sequences with no query this step (query_start_loc with q_len 0);
-  - repeated calls on one workspace (the arrival counters must reset), and
-    the counter region must be all zero after every call.
+  - repeated calls on one workspace (per-sequence records of one call must
+    never leak into the next, e.g. a sequence without a query this step).
 bf16/fp16 tolerance 2e-2 absolute (bf16 P in the PV product).
 """
 import numpy as np
@@ -48,11 +48,6 @@ def check(out, lse, eo, el, what):
         np.testing.assert_allclose(L[fin], el[fin], rtol=0, atol=2e-2, err_msg=what)
 
 
-def counters_zero():
-    for buf in _native.WORKSPACE._bufs.values():
-        assert not buf[: 256 * 1024].any(), "arrival counters not left at zero"
-
-
 @pytest.mark.parametrize("g,d", SHAPES)
 @pytest.mark.parametrize("part_tokens", [SK, 0, 512])
 def test_single_long_sequence(g, d, part_tokens):
@@ -64,7 +59,6 @@ def test_single_long_sequence(g, d, part_tokens):
     torch.cuda.synchronize()
     eo, el = oracle(p)
     check(out, lse, eo, el, "long")
-    counters_zero()
 
 
 @pytest.mark.parametrize("g,d", SHAPES)
@@ -84,7 +78,6 @@ def test_many_short_and_empty_sequences_repeated(g, d):
                                part_tokens=SK)
         torch.cuda.synchronize()
         check(out, lse, eo, el, f"short rep {rep}")
-        counters_zero()
     # the partition kernel agrees
     out2 = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, part_tokens=256)
     check(out2, None, eo, el, "partition kernel")
@@ -110,8 +103,7 @@ def test_gqa_two_kv_heads_and_missing_queries(dtype):
                          query_start_loc=qsl, part_tokens=pt)
         torch.cuda.synchronize()
         check(O, L, eo, el, f"gqa part_tokens={pt}")
-        counters_zero()
-
+    
 
 def test_cfg4_and_cfg5_kernels_agree():
     for name, p in [("cfg4", workloads.cfg4_problem(DEV)), ("cfg5", workloads.cfg5_problem(DEV))]:
@@ -123,4 +115,31 @@ def test_cfg4_and_cfg5_kernels_agree():
         torch.cuda.synchronize()
         diff = (a.float() - b.float()).abs().max().item()
         assert diff <= 2e-2, f"{name}: persistent vs partition kernel differ by {diff}"
-        counters_zero()
+    
+
+def test_records_of_previous_call_do_not_leak():
+    """A call where every sequence is split across workgroups, then a call on
+    the same workspace where some of those sequences have no query: rows are
+    written only for the queries present (a guard row past T stays intact)."""
+    g, d = 32, 128
+    lens = [6000, 5000, 7000, 4000, 6500]
+    p = workloads.decode_problem(lens, g, 1, d, 16, 4096, torch.bfloat16, DEV, seed=14)
+    first = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens,
+                             part_tokens=SK)
+    torch.cuda.synchronize()
+    eo, el = oracle(p)
+    check(first, None, eo, el, "all queries")
+    qlens = [0, 1, 0, 1, 1]
+    qsl = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device=DEV)
+    T = int(sum(qlens))
+    q = p.q[[1, 3, 4]].contiguous()
+    out = torch.full((T + 1, g, d), 7.0, dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((T + 1, g), 7.0, device=DEV)
+    paged_mqa_decode(q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, out=out[:T],
+                     lse=lse[:T], part_tokens=SK, query_start_loc=qsl)
+    torch.cuda.synchronize()
+    eo2, el2 = ref.paged_attention(np64(q), np64(p.k_pool), np64(p.v_pool),
+                                   p.block_tables.cpu().numpy(), p.seq_lens.cpu().numpy(),
+                                   qsl.cpu().numpy())
+    check(out[:T], lse[:T], eo2, el2, "subset of queries")
+    assert torch.all(out[T] == 7.0) and torch.all(lse[T] == 7.0), "guard row overwritten"

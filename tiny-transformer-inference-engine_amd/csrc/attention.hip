@@ -224,21 +224,36 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a,
   const int64_t qrow = (int64_t)(g.q_begin + i) * a.hq + kvh * G + h;
   const int64_t unit0 = ((int64_t)blockIdx.x * a.tiles_max + tile) * a.parts_max;
   T* __restrict__ out = static_cast<T*>(a.out) + qrow * D + d0;
+  // one pass with a running max; the loads of kMB partitions are issued
+  // before any is consumed and never sit under a branch (a branch join
+  // would make the compiler wait for every load issued before it), so the
+  // merge costs ceil(nparts / kMB) memory latencies
+  constexpr int kMB = 8;
   float M = -INFINITY;
-  for (int p = 0; p < g.nparts; ++p)
-    M = fmaxf(M, a.ws_ml[((unit0 + p) * rows_per_tile + r) * 2]);
   float L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (M != -INFINITY) {
-    for (int p = 0; p < g.nparts; ++p) {
-      const int64_t row = (unit0 + p) * rows_per_tile + r;
-      const float wt = exp2f(a.ws_ml[row * 2] - M);
-      L = fmaf(a.ws_ml[row * 2 + 1], wt, L);
-      const float4 o = *reinterpret_cast<const float4*>(a.ws_o + row * D + d0);
-      acc.x = fmaf(o.x, wt, acc.x);
-      acc.y = fmaf(o.y, wt, acc.y);
-      acc.z = fmaf(o.z, wt, acc.z);
-      acc.w = fmaf(o.w, wt, acc.w);
+  for (int p0 = 0; p0 < g.nparts; p0 += kMB) {
+    float mm[kMB], ll[kMB];
+    float4 oo[kMB];
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      const int64_t row = (unit0 + min(p0 + j, g.nparts - 1)) * rows_per_tile + r;
+      mm[j] = a.ws_ml[row * 2];
+      ll[j] = a.ws_ml[row * 2 + 1];
+      oo[j] = *reinterpret_cast<const float4*>(a.ws_o + row * D + d0);
+    }
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      if (p0 + j >= g.nparts || mm[j] == -INFINITY) continue;
+      const float Mn = fmaxf(M, mm[j]);
+      const float sa = exp2f(M - Mn);
+      const float sb = exp2f(mm[j] - Mn);
+      L = L * sa + ll[j] * sb;
+      acc.x = acc.x * sa + oo[j].x * sb;
+      acc.y = acc.y * sa + oo[j].y * sb;
+      acc.z = acc.z * sa + oo[j].z * sb;
+      acc.w = acc.w * sa + oo[j].w * sb;
+      M = Mn;
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -284,6 +299,10 @@ int ceil_div_h(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 }  // namespace
 
+// Whether the persistent kernel takes this problem: one record per
+// (sequence, kv head) pair fits the workspace's record region.
+bool sk_fits(int64_t virt) { return virt >= 1 && virt <= kMaxCounters; }
+
 AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,
                         int part_tokens, int dtype) {
@@ -291,7 +310,14 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   const int group = hq / hkv;
   const bool mfma = decode_mfma_supported(dtype, max_q_len, group, d);
   const int64_t virt = (int64_t)n_seq * hkv;
-  if (mfma && part_tokens == PKV_PART_PERSISTENT && virt <= kMaxCounters) {
+  const int64_t cap_tokens = (int64_t)max_blk * block_size;
+  const int64_t kv_bound = max_kv_len > 0 && max_kv_len < cap_tokens ? max_kv_len : cap_tokens;
+  // automatic choice: long context bounds (where fixed-length partitions
+  // leave the long sequences' workgroups running alone) take the persistent
+  // kernel, which gives every workgroup the same share of the actual work
+  const bool persistent = part_tokens == PKV_PART_PERSISTENT ||
+                          (part_tokens == 0 && kv_bound >= kSkAutoKv);
+  if (mfma && persistent && sk_fits(virt)) {
     // persistent kernel: partials of at most two segments per workgroup
     p.kind = 2;
     p.rows = group;
@@ -360,10 +386,11 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
   if (p.kind == 2) {
     SkArgs k{};
     k.n_wg = 2 * device_cu_count() < kSkMaxWg ? 2 * device_cu_count() : kSkMaxWg;
+    k.seg_cost = kSkSegCost;
     char* ws = reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes;
-    k.counters = reinterpret_cast<int*>(ws);
+    k.recs = reinterpret_cast<int4*>(ws);
     k.part_o = a.ws_o;
-    k.part_ml = a.ws_o + (size_t)kSkMaxWg * 2 * a.group * a.d;
+    k.part_ml = k.part_o + (size_t)kSkMaxWg * 2 * a.group * a.d;
     return launch_decode_sk(a, k, dtype, stream);
   }
   if (p.kind == 1) {

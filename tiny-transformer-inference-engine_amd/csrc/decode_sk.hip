@@ -1,19 +1,23 @@
 // Paged MQA decode, persistent form: two 4-wavefront workgroups per CU, each
-// owning an equal contiguous share of all sequences' 32-token chunks.
+// owning an equal share of all sequences' work.
 //
-// The chunks of every (sequence, kv head) pair are laid end to end; with C
-// chunks in total and W workgroups, workgroup w owns global chunks
-// [R(w), R(w+1)), R(w) = floor(w C / W). Every workgroup streams the same
-// amount of K/V whatever the length distribution, no workgroup is launched
-// without work, and a single launch does everything:
+// Every (sequence, kv head) pair v with a query is laid end to end on a cost
+// line as K overhead units (its Q load, table slice, wavefront merge and
+// output, worth about K chunks of streaming) followed by its n_v 32-token
+// chunks. With C units in total and W workgroups, workgroup w owns units
+// [R(w), R(w+1)), R(w) = floor(w C / W), and processes the chunks among
+// them. Every workgroup gets the same amount of work whatever the length
+// distribution (one that covers many short sequences streams fewer chunks):
 //   - a sequence that lies entirely inside one share is finished in place
 //     (its wavefronts' states are merged through LDS and written out);
 //   - a sequence cut by share boundaries gets one partial (m, l, O) per
 //     workgroup that touches it (its first or last segment there, so at most
-//     two per workgroup); each writer releases its partial and counts itself
-//     on the sequence's arrival counter, and the last to arrive merges all of
-//     them and resets the counter to zero for the next launch. Nobody waits,
-//     so the scheme cannot deadlock whatever the residency.
+//     two per workgroup), written with plain stores; the workgroup holding
+//     its first chunk also records which workgroups contributed.
+// sk_merge_kernel, launched right after on the same stream (the kernel
+// boundary makes the partials visible), combines the partials of every cut
+// sequence in parallel over (sequence, output slice). Nothing waits on
+// another workgroup, so the scheme cannot deadlock whatever the residency.
 // The per-chunk pipeline is mfma_decode_common.h. Semantics are those of
 // pagedattn.forward (kernels/pagedattn/pagedattn.cu:142-447) for q_len = 1.
 #include "mfma_decode_common.h"
@@ -59,35 +63,9 @@ __device__ __forceinline__ int share_owner(int x, int C, int W) {
   return (int)(((int64_t)(x + 1) * W - 1) / C);
 }
 
-// Partials cross workgroups that may sit on different XCDs, whose L2s are not
-// coherent with each other. They are written and read with system-scope
-// relaxed accesses, which go through to memory (write-through stores,
-// cache-bypassing loads) instead of relying on whole-L2 writeback /
-// invalidate fences.
-__device__ __forceinline__ void coherent_store2(float* p, float x, float y) {
-  union { float f[2]; unsigned long long u; } b;
-  b.f[0] = x;
-  b.f[1] = y;
-  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), b.u, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ void coherent_load2(const float* p, float& x, float& y) {
-  union { float f[2]; unsigned long long u; } b;
-  b.u = __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float*>(p)),
-                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  x = b.f[0];
-  y = b.f[1];
-}
-
-// Partial slot that workgroup ww wrote for the sequence whose chunk 0 is
-// global chunk g0, w_first being the workgroup owning g0: the sequence is
-// the first segment of every contributor except possibly w_first, where it
-// is the last segment unless w_first's share starts exactly at g0.
-__device__ __forceinline__ int partial_slot(int ww, int w_first, int g0, int C, int W);
-
-__device__ __forceinline__ int partial_slot(int ww, int w_first, int g0, int C, int W) {
-  return 2 * ww + (ww == w_first && share_start(ww, C, W) != g0 ? 1 : 0);
-}
+// Cost of virtual sequence v on the share line: 0 without a query, else
+// seg_cost overhead units plus its chunks.
+__device__ __forceinline__ int sk_cost(int n, int seg_cost) { return n > 0 ? n + seg_cost : 0; }
 
 // block-wide exclusive scan of one int per thread; returns the total
 __device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
@@ -122,7 +100,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   __shared__ float ml_lds[kWaves][G][2];
   __shared__ int tbl[kTblCap];
   __shared__ int scan_sh[kBlock];
-  __shared__ int s_v0, s_off0, s_g0, s_last;
+  __shared__ int s_v0, s_g0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -132,38 +110,49 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   const int wg = blockIdx.x;
   const int V = a.n_seq * a.hkv;
 
-  // ---- total chunk count C, then the sequence holding this share's start
+  // ---- total cost C, then the sequence whose cost interval holds this
+  // share's start (the first pass's values are kept when V fits one block)
+  const int K = k.seg_cost;
   int C = 0;
+  int n_mine = 0, ex_mine = 0;
   for (int base = 0; base < V; base += kBlock) {
     int kl;
-    const int n = base + tid < V ? sk_chunks(a, base + tid, kl) : 0;
+    const int n = base + tid < V ? sk_cost(sk_chunks(a, base + tid, kl), K) : 0;
     int ex;
     C += block_scan(n, scan_sh, ex);
+    n_mine = n;
+    ex_mine = ex;
   }
-  // at most one share per chunk, so that every share is non-empty (the
-  // mergers count and read exactly the workgroups that wrote a partial)
+  // at most one share per unit, so that every share is non-empty
   const int W = k.n_wg < C ? k.n_wg : C;
   if (wg >= W) return;
   const int start = share_start(wg, C, W);
   const int end = share_start(wg + 1, C, W);
   if (tid == 0) s_v0 = -1;
   __syncthreads();
-  int run = 0;
-  for (int base = 0; base < V; base += kBlock) {
-    int kl;
-    const int v = base + tid;
-    const int n = v < V ? sk_chunks(a, v, kl) : 0;
-    int ex;
-    const int tot = block_scan(n, scan_sh, ex);
-    if (n > 0 && run + ex <= start && start < run + ex + n) {
-      s_v0 = v;
-      s_off0 = start - (run + ex);
-      s_g0 = run + ex;
+  if (V <= kBlock) {
+    if (n_mine > 0 && ex_mine <= start && start < ex_mine + n_mine) {
+      s_v0 = tid;
+      s_g0 = ex_mine;
     }
-    run += tot;
-    __syncthreads();
-    if (s_v0 >= 0) break;
+  } else {
+    int run = 0;
+    for (int base = 0; base < V; base += kBlock) {
+      int kl;
+      const int v = base + tid;
+      const int n = v < V ? sk_cost(sk_chunks(a, v, kl), K) : 0;
+      int ex;
+      const int tot = block_scan(n, scan_sh, ex);
+      if (n > 0 && run + ex <= start && start < run + ex + n) {
+        s_v0 = v;
+        s_g0 = run + ex;
+      }
+      run += tot;
+      __syncthreads();
+      if (s_v0 >= 0) break;
+    }
   }
+  __syncthreads();
 
   PoolView pv;
   pv.kbase = static_cast<const char*>(a.k_pool);
@@ -189,18 +178,19 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   const int win = (kTblCap - 1) << a.bs_shift;
 
   int v = s_v0;
-  int c0 = s_off0;
-  int g0 = s_g0;  // global index of chunk 0 of sequence v
-  int remaining = end - start;
+  int g0 = s_g0;  // cost position where sequence v's interval starts
   bool first = true;
-  while (remaining > 0) {
+  // sequence v's chunks sit at units [g0 + K, g0 + K + n); the share's
+  // chunks are those among [start, end)
+  while (g0 + K < end) {
     int kv_len;
     const int n = sk_chunks(a, v, kv_len);
     if (n == 0) {
       ++v;
       continue;
     }
-    const int c1 = min(n, c0 + remaining);
+    const int c0 = max(0, start - (g0 + K));
+    const int c1 = min(n, end - (g0 + K));
     const bool whole = c0 == 0 && c1 == n;
     const int s = v / a.hkv;
     const int kvh = v - s * a.hkv;
@@ -273,121 +263,121 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
         dst[3] = (T)(acc[3] * inv);
         if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
       } else {
-        // written through to memory (system-coherent stores), so another
-        // XCD's L2 can never hold a stale copy and no cache flush is needed
-        float* po = k.part_o + ((int64_t)slot * G + head) * D + d0;
-        coherent_store2(po, acc[0], acc[1]);
-        coherent_store2(po + 2, acc[2], acc[3]);
-        if (d0 == 0) coherent_store2(k.part_ml + ((int64_t)slot * G + head) * 2, M, L);
+        *reinterpret_cast<floatx4*>(k.part_o + ((int64_t)slot * G + head) * D + d0) = acc;
+        if (d0 == 0) {
+          k.part_ml[((int64_t)slot * G + head) * 2 + 0] = M;
+          k.part_ml[((int64_t)slot * G + head) * 2 + 1] = L;
+        }
       }
     }
 
-    if (!whole) {
-      // every thread's write-through stores are complete before the
-      // workgroup counts itself; the count and the merger's reads go to the
-      // memory side too, so the last arrival sees every partial
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      const int w_first = share_owner(g0, C, W);
-      const int w_last = share_owner(g0 + n - 1, C, W);
-      if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(k.counters + v, 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_SYSTEM);
-        s_last = old == w_last - w_first;
-      }
-      __syncthreads();
-      if (s_last) {
-        // contributors' loads are issued in unrolled batches of kMB before
-        // any is consumed, so a sequence cut into many shares costs a few
-        // memory latencies, not one per contributor
-        constexpr int kMB = 8;
-        for (int idx = tid; idx < G * D / 4; idx += kBlock) {
-          const int head = idx / (D / 4);
-          const int d0 = (idx - head * (D / 4)) * 4;
-          float M = -INFINITY;
-          for (int wb = w_first; wb <= w_last; wb += kMB) {
-            float mm[kMB], ll[kMB];
-#pragma unroll
-            for (int i = 0; i < kMB; ++i) {
-              mm[i] = -INFINITY;
-              if (wb + i <= w_last)
-                coherent_load2(k.part_ml + ((int64_t)partial_slot(wb + i, w_first, g0, C, W) * G +
-                                            head) * 2, mm[i], ll[i]);
-            }
-#pragma unroll
-            for (int i = 0; i < kMB; ++i) M = fmaxf(M, mm[i]);
-          }
-          float L = 0.f;
-          floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-          if (M != -INFINITY) {
-            for (int wb = w_first; wb <= w_last; wb += kMB) {
-              float mm[kMB], ll[kMB], o0[kMB], o1[kMB], o2[kMB], o3[kMB];
-#pragma unroll
-              for (int i = 0; i < kMB; ++i) {
-                mm[i] = -INFINITY;
-                ll[i] = o0[i] = o1[i] = o2[i] = o3[i] = 0.f;
-                if (wb + i <= w_last) {
-                  const int64_t sl = partial_slot(wb + i, w_first, g0, C, W);
-                  coherent_load2(k.part_ml + (sl * G + head) * 2, mm[i], ll[i]);
-                  const float* po = k.part_o + (sl * G + head) * D + d0;
-                  coherent_load2(po, o0[i], o1[i]);
-                  coherent_load2(po + 2, o2[i], o3[i]);
-                }
-              }
-#pragma unroll
-              for (int i = 0; i < kMB; ++i) {
-                const float wt = mm[i] == -INFINITY ? 0.f : exp2f(mm[i] - M);
-                L += ll[i] * wt;
-                acc[0] += o0[i] * wt;
-                acc[1] += o1[i] * wt;
-                acc[2] += o2[i] * wt;
-                acc[3] += o3[i] * wt;
-              }
-            }
-          }
-          const int64_t qrow = qrow0 + head;
-          const float inv = L > 0.f ? 1.f / L : 0.f;
-          T* dst = out + qrow * D + d0;
-          dst[0] = (T)(acc[0] * inv);
-          dst[1] = (T)(acc[1] * inv);
-          dst[2] = (T)(acc[2] * inv);
-          dst[3] = (T)(acc[3] * inv);
-          if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
-        }
-        if (tid == 0)  // ready for the next launch
-          __hip_atomic_store(k.counters + v, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      }
+    if (c0 == 0 && tid == 0) {
+      // contributors of this sequence, for the merge kernel
+      const int w_first = share_owner(g0 + K, C, W);
+      const int w_last = share_owner(g0 + K + n - 1, C, W);
+      k.recs[v] = make_int4(w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0, 0);
     }
     __syncthreads();  // LDS merge area is reused by the next segment
 
-    remaining -= c1 - c0;
-    g0 += n;
+    g0 += n + K;
     ++v;
-    c0 = 0;
     first = false;
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
 }
 
+// Combines the partials of every sequence cut by share boundaries: one
+// thread per (sequence, head, 4 output dims), contributors' loads issued in
+// batches of kMB before any is consumed, running max per head.
+constexpr int kMergeBlock = 256;
+template <typename T, int G, int D>
+__global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArgs k) {
+  const int v = blockIdx.x;
+  int kv_len;
+  if (sk_chunks(a, v, kv_len) == 0) return;  // no query: nothing was recorded
+  const int4 r = k.recs[v];
+  const int w_first = r.x, w_last = r.y;
+  if (w_last <= w_first) return;  // finished in place
+  const int idx = blockIdx.y * kMergeBlock + threadIdx.x;
+  if (idx >= G * D / 4) return;
+  const int head = idx / (D / 4);
+  const int d0 = (idx - head * (D / 4)) * 4;
+  constexpr int kMB = 8;
+  float M = -INFINITY, L = 0.f;
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int wb = w_first; wb <= w_last; wb += kMB) {
+    float mm[kMB], ll[kMB];
+    floatx4 oo[kMB];
+    // branch-free: contributors past w_last re-read w_last's partial and are
+    // dropped afterwards, so no load sits under a branch (a branch join
+    // would make the compiler wait for every load issued before it)
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      const int ww = min(wb + j, w_last);
+      const int64_t sl = ww == w_first ? 2 * ww + r.z : 2 * ww;
+      mm[j] = k.part_ml[(sl * G + head) * 2 + 0];
+      ll[j] = k.part_ml[(sl * G + head) * 2 + 1];
+      oo[j] = *reinterpret_cast<const floatx4*>(k.part_o + (sl * G + head) * D + d0);
+    }
+#pragma unroll
+    for (int j = 0; j < kMB; ++j)
+      if (wb + j > w_last) mm[j] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      if (mm[j] == -INFINITY) continue;
+      const float Mn = fmaxf(M, mm[j]);
+      const float sa = exp2f(M - Mn);
+      const float sb = exp2f(mm[j] - Mn);
+      L = L * sa + ll[j] * sb;
+      acc = acc * sa + oo[j] * sb;
+      M = Mn;
+    }
+  }
+  const int s = v / a.hkv;
+  const int kvh = v - s * a.hkv;
+  const int64_t qrow = (int64_t)(a.qloc ? a.qloc[s] : s) * a.hq + kvh * G + head;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  T* dst = static_cast<T*>(a.out) + qrow * D + d0;
+  dst[0] = (T)(acc[0] * inv);
+  dst[1] = (T)(acc[1] * inv);
+  dst[2] = (T)(acc[2] * inv);
+  dst[3] = (T)(acc[3] * inv);
+  if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
+}
+
+template <typename T, int D, int NT, int PF, bool OFF64>
+int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
+  k.n_wg = sk_workgroups(D, 16 * NT);
+  hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64>), dim3(k.n_wg), dim3(kBlock), 0,
+                     stream, a, k);
+  int rc = check_launch("decode_sk_kernel");
+  if (rc != PKV_OK) return rc;
+  constexpr int G = 16 * NT;
+  const dim3 mgrid(a.n_seq * a.hkv, (G * D / 4 + kMergeBlock - 1) / kMergeBlock);
+  hipLaunchKernelGGL((sk_merge_kernel<T, G, D>), mgrid, dim3(kMergeBlock), 0, stream, a, k);
+  return check_launch("sk_merge_kernel");
+}
+
 template <typename T, bool OFF64>
 int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
-  const dim3 grid(k.n_wg);
   const int nt = a.group / 16;
-  // <T, D, NT, PF, OFF64>: two wavefronts per SIMD (8 per CU, two workgroups)
-  if (a.d == 64 && nt == 1)
-    hipLaunchKernelGGL((decode_sk_kernel<T, 64, 1, 2, OFF64>), grid, dim3(kBlock), 0, stream, a, k);
-  else if (a.d == 64 && nt == 2)
-    hipLaunchKernelGGL((decode_sk_kernel<T, 64, 2, 2, OFF64>), grid, dim3(kBlock), 0, stream, a, k);
-  else if (a.d == 128 && nt == 1)
-    hipLaunchKernelGGL((decode_sk_kernel<T, 128, 1, 1, OFF64>), grid, dim3(kBlock), 0, stream, a, k);
-  else if (a.d == 128 && nt == 2)
-    hipLaunchKernelGGL((decode_sk_kernel<T, 128, 2, 1, OFF64>), grid, dim3(kBlock), 0, stream, a, k);
-  else
-    return fail(PKV_ERR_UNSUPPORTED, "decode_sk: d=%d group=%d", a.d, a.group);
-  return check_launch("decode_sk_kernel");
+  // <T, D, NT, PF, OFF64>: two wavefronts per SIMD; the D = 128 variants
+  // have room for one chunk in flight per wavefront, the D = 64 ones for two
+  if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, OFF64>(a, k, stream);
+  if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, OFF64>(a, k, stream);
+  if (a.d == 128 && nt == 1) return launch_v<T, 128, 1, 1, OFF64>(a, k, stream);
+  if (a.d == 128 && nt == 2) return launch_v<T, 128, 2, 1, OFF64>(a, k, stream);
+  return fail(PKV_ERR_UNSUPPORTED, "decode_sk: d=%d group=%d", a.d, a.group);
 }
 
 }  // namespace
+
+int sk_workgroups(int d, int group) {
+  (void)d;
+  (void)group;
+  const int n = 2 * device_cu_count();
+  return n < kSkMaxWg ? n : kSkMaxWg;
+}
 
 int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream) {
   if (a.num_blocks >= (int64_t(1) << 31))

@@ -48,6 +48,7 @@ struct Ops<f16> {
 };
 
 constexpr int kTblCap = 256;  // block-table entries staged in LDS at a time
+constexpr float kLazy = 8.f;  // log2 headroom of the lazily moved softmax reference
 constexpr float kLn2f = 0.6931471805599453f;
 
 // LDS geometry of one 32-token chunk of K (or V) rows, D bf16/fp16 each.
@@ -120,6 +121,7 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NPL>& r, const PoolView& pv
   for (int j = 0; j < NPL; ++j) {
     int pos = cb + cx.prow + j * Geo::ROWS_PER_LOAD;
     pos = pos < cx.seg_hi ? pos : cx.seg_hi - 1;
+    pos = pos > 0 ? pos : 0;  // an empty context (seg_hi = 0) reads row 0
     const int phys = cx.tbl[(pos >> pv.bs_shift) - cx.blk_lo];
     const bool ok = (unsigned)phys < (unsigned)pv.num_blocks;
     vmask |= (unsigned)ok << j;
@@ -156,17 +158,11 @@ struct WaveState {
   }
 };
 
-// One chunk: registers -> LDS slice, optionally refill the registers with
-// chunk `c + ahead`, then QK / softmax / PV out of LDS.
-template <typename T, int D, int NT, int NPL, bool OFF64>
-__device__ __forceinline__ void chunk_step(
-    ChunkRegs<NPL>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
-    const PoolView& pv, const typename Ops<T>::v8 (&qf)[NT][D / 32],
-    WaveState<NT, D / 16>& st, bool& bad_block) {
-  using Geo = ChunkGeo<D>;
-  using v8 = typename Ops<T>::v8;
-  constexpr int KS = D / 32;
-  constexpr int DT = D / 16;
+// Registers -> this wavefront's LDS slice (rows with a bad table entry are
+// zeroed and flagged).
+template <class Geo, int NPL>
+__device__ __forceinline__ void stage_chunk(const ChunkRegs<NPL>& r, const ChunkCtx& cx,
+                                            bool& bad_block) {
   asm volatile("" ::: "memory");
   const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
@@ -177,13 +173,20 @@ __device__ __forceinline__ void chunk_step(
     *reinterpret_cast<u32x4*>(cx.kl + Geo::off(row, cx.pcol)) = ok ? r.k[j] : zero;
     *reinterpret_cast<u32x4*>(cx.vl + Geo::off(row, cx.pcol)) = ok ? r.v[j] : zero;
   }
-  if (refill) load_chunk<Geo, NPL, OFF64>(r, pv, cx, c + ahead);
+}
+
+// S^T = K Q^T of the chunk staged in cx's K slice: tokens 16h + 4*grp + r
+// of the chunk for head 16nt + l16.
+template <typename T, int D, int NT>
+__device__ __forceinline__ void chunk_scores(const ChunkCtx& cx,
+                                             const typename Ops<T>::v8 (&qf)[NT][D / 32],
+                                             floatx4 (&sacc)[NT][2]) {
+  using Geo = ChunkGeo<D>;
+  using v8 = typename Ops<T>::v8;
+  constexpr int KS = D / 32;
   // the slice is private to this wavefront: waiting for its own LDS writes
   // is the only synchronisation the reads below need
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-
-  // S^T = K Q^T, tokens 16h + 4*grp + r of this chunk for head 16nt + l16
-  floatx4 sacc[NT][2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     v8 kf[KS];
@@ -198,13 +201,29 @@ __device__ __forceinline__ void chunk_step(
       sacc[nt][h] = acc;
     }
   }
+}
 
-  // online softmax (base 2); P^T operand = this lane's 8 probabilities
+// Softmax update and O^T += V^T P^T for the chunk whose scores are sacc:
+// tokens seg_lo + 32c ..., those at or past seg_hi masked out.
+template <typename T, int D, int NT>
+__device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
+                                             const floatx4 (&sacc)[NT][2],
+                                             WaveState<NT, D / 16>& st) {
+  using Geo = ChunkGeo<D>;
+  using v8 = typename Ops<T>::v8;
+  constexpr int DT = D / 16;
+
+  // online softmax (base 2) with a lazily moved reference: probabilities
+  // are taken relative to st.m, which only moves (with the head-wide max
+  // shuffles and the rescale of l and O) when some score of the wavefront
+  // exceeds it by more than kLazy; so p <= 2^kLazy, exact in bf16/fp16
+  // relative terms, and most chunks skip the shuffles and the rescale.
+  // P^T operand = this lane's 8 probabilities.
   const int cb = cx.seg_lo + c * kChunk;
-  v8 pf[NT];
+  float sv[NT][8];
+  bool move = false;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    float sv[8];
     float mx = -INFINITY;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -212,25 +231,39 @@ __device__ __forceinline__ void chunk_step(
       for (int rr = 0; rr < 4; ++rr) {
         const int pos = cb + 16 * h + 4 * cx.grp + rr;
         const float x = pos < cx.seg_hi ? sacc[nt][h][rr] * cx.scale_log2 : -INFINITY;
-        sv[4 * h + rr] = x;
+        sv[nt][4 * h + rr] = x;
         mx = fmaxf(mx, x);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(st.m[nt], mx);
-    const float ref = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(st.m[nt] - ref);
+    move |= mx > st.m[nt] + kLazy;  // also true on the first scores (m = -inf)
+  }
+  if (__builtin_amdgcn_ballot_w64(move) != 0) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sv[nt][e]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(st.m[nt], mx);
+      const float alpha = m_new == -INFINITY ? 1.f : exp2f(st.m[nt] - m_new);
+      st.l[nt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) st.o[nt][dt] *= alpha;
+      st.m[nt] = m_new;
+    }
+  }
+  v8 pf[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float ref = st.m[nt] == -INFINITY ? 0.f : st.m[nt];
     float ps = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float p = exp2f(sv[e] - ref);
+      const float p = exp2f(sv[nt][e] - ref);
       ps += p;
       pf[nt][e] = (T)p;
     }
-    st.l[nt] = st.l[nt] * alpha + ps;
-    st.m[nt] = m_new;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) st.o[nt][dt] *= alpha;
+    st.l[nt] += ps;
   }
 
   // O^T += V^T P^T; V^T fragment: dims 16dt + l16, the same 8 tokens
@@ -246,6 +279,30 @@ __device__ __forceinline__ void chunk_step(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) st.o[nt][dt] = Ops<T>::mma(vf, pf[nt], st.o[nt][dt]);
   }
+}
+
+// QK / softmax / PV of the chunk staged in cx's slices.
+template <typename T, int D, int NT>
+__device__ __forceinline__ void compute_chunk(int c, const ChunkCtx& cx,
+                                              const typename Ops<T>::v8 (&qf)[NT][D / 32],
+                                              WaveState<NT, D / 16>& st) {
+  floatx4 sacc[NT][2];
+  chunk_scores<T, D, NT>(cx, qf, sacc);
+  chunk_update<T, D, NT>(c, cx, sacc, st);
+}
+
+// One chunk: registers -> LDS slice, optionally refill the registers with
+// chunk `c + ahead` (issued before any compute so the loads overlap it),
+// then QK / softmax / PV out of LDS.
+template <typename T, int D, int NT, int NPL, bool OFF64>
+__device__ __forceinline__ void chunk_step(
+    ChunkRegs<NPL>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
+    const PoolView& pv, const typename Ops<T>::v8 (&qf)[NT][D / 32],
+    WaveState<NT, D / 16>& st, bool& bad_block) {
+  using Geo = ChunkGeo<D>;
+  stage_chunk<Geo, NPL>(r, cx, bad_block);
+  if (refill) load_chunk<Geo, NPL, OFF64>(r, pv, cx, c + ahead);
+  compute_chunk<T, D, NT>(c, cx, qf, st);
 }
 
 // All chunks of [cx.seg_lo, cx.seg_hi) assigned to wavefront w of nw:
@@ -291,12 +348,13 @@ template <typename T, int D, int NT>
 __device__ __forceinline__ void load_q(typename Ops<T>::v8 (&qf)[NT][D / 32], const T* q,
                                        int64_t qrow0, int grp, int l16) {
   using v8 = typename Ops<T>::v8;
+  const T* __restrict__ base = q + qrow0 * D;  // wavefront-uniform
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks)
-      qf[nt][ks] = *reinterpret_cast<const v8*>(q + (qrow0 + 16 * nt + l16) * D +
-                                               (4 * ks + grp) * 8);
+      qf[nt][ks] = *reinterpret_cast<const v8*>(
+          base + (unsigned)((16 * nt + l16) * D + (4 * ks + grp) * 8));
 }
 
 }  // namespace mfma

@@ -81,16 +81,23 @@ constexpr int kGenRows = 32;
 constexpr int kChunk = 32;  // kv tokens staged per iteration
 
 // Workspace layout: the first kWsCounterBytes hold the persistent decode
-// kernel's arrival counters (one int per sequence x kv head). They must be
-// zero before the first call and every call leaves them zero; no other
-// kernel touches them. Partials start after them.
+// kernel's per-sequence records (which workgroups hold partials of each
+// (sequence, kv head)); they are written before they are read in every call,
+// so they need no initialisation. Partials start after them.
 constexpr size_t kWsCounterBytes = 256 * 1024;
-constexpr int kMaxCounters = (int)(kWsCounterBytes / sizeof(int));
+constexpr int kMaxCounters = (int)(kWsCounterBytes / sizeof(int4));
 constexpr int kSkMaxWg = 512;  // workgroups of the persistent kernel, at most
+// A sequence's fixed cost in the persistent kernel (Q load, table slice,
+// wavefront merge, output or partial write) measured in 32-token chunks of
+// one workgroup's streaming time.
+constexpr int kSkSegCost = 3;
+// Context bound from which part_tokens = 0 selects the persistent kernel.
+constexpr int kSkAutoKv = 4096;
 
 struct SkArgs {
-  int n_wg;         // workgroups launched (one per CU)
-  int* counters;    // [n_seq * hkv] arrival counters
+  int n_wg;         // workgroups launched
+  int seg_cost;     // overhead of one sequence in chunk units (share balance)
+  int4* recs;       // [n_seq * hkv] (first, last contributor, first's slot)
   float* part_o;    // [n_wg][2][G][D] partial outputs
   float* part_ml;   // [n_wg][2][G][2] partial (max, sum)
 };
@@ -162,6 +169,8 @@ bool pool_needs_off64(const AttnArgs& a);
 int launch_decode_mfma(const AttnArgs& a, const AttnPlan& plan, int dtype,
                        hipStream_t stream);
 // Persistent MFMA decode kernel (decode_sk.hip), same coverage.
+// Workgroups the persistent kernel launches for this head shape.
+int sk_workgroups(int d, int group);
 int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream);
 // CUs of the current device (cached; 256 when no device is visible).
 int device_cu_count();

@@ -121,7 +121,7 @@ def ptr(t) -> int | None:
 
 class Workspace:
     """Per-device scratch for split-K partials and the persistent kernel's
-    arrival counters, grown on demand and reused (the library never
+    per-sequence records, grown on demand and reused (the library never
     allocates). Allocation goes through torch's caching allocator, so it is
     stream-ordered on the current stream; calls on other streams need their
     own Workspace."""
@@ -137,9 +137,8 @@ class Workspace:
         if buf is None or buf.numel() < nbytes:
             # grow geometrically so ragged batches do not reallocate every step
             size = max(nbytes, 0 if buf is None else 2 * buf.numel())
-            # zeroed: the leading counter region must start at zero (the
-            # kernels leave it zero after every call)
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            # every call writes what it reads back: no initialisation needed
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
             self._bufs[idx] = buf
         return buf
 
