@@ -40,6 +40,7 @@ for _p in (PKG, REPO):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+N_MODEL = 128  # decode batch of the model step
 METRIC = "paged MQA decode HBM GB/s (% of peak); decode tok/s at batch 128"
 
 
@@ -153,13 +154,16 @@ def run_model(args, torch):
     model = PagedTransformer(cfg).to(dev, torch.bfloat16).eval()
     N, BS, NB = 128, 16, 16384
     lens = workloads.lengths_uniform(N, 256, 2048, seed=0)
-    tables = cfg4_tables(lens, BS, NB, steps + args.warmup + 1, seed=0)
+    tables = cfg4_tables(lens, BS, NB, 2 * steps + args.warmup + 8, seed=0)
     pool = KVPool(cfg.num_layers, BS, NB, 1, cfg.head_dim, torch.bfloat16, dev)
     g = torch.Generator(device=dev).manual_seed(1)
     for l in range(cfg.num_layers):
         pool.kv[l].normal_(generator=g)
     meta = pack_batch_meta(tables, list(range(N + 1)), [int(x) for x in lens], N, dev, BS)
     ids = torch.randint(0, cfg.vocab_size, (N,), generator=g, device=dev)
+
+    # plan the attention for the context the batch reaches by the last step
+    meta.max_kv_len = int(max(lens)) + 2 * steps + args.warmup + 8
 
     def step():
         nonlocal ids
@@ -169,15 +173,23 @@ def run_model(args, torch):
         meta.positions.add_(1)
         meta.start_pos.add_(1)
         meta.seq_lens.add_(1)
-        meta.max_kv_len += 1
 
+    stream = torch.cuda.current_stream(dev)
     with torch.no_grad():
-        for _ in range(args.warmup):
+        for _ in range(2):
             step()
         torch.cuda.synchronize()
-        sec = time_events(step, steps, torch.cuda.current_stream(dev))
-    log(f"model decode step: {sec * 1e3:.3f} ms, {N / sec:.0f} tok/s")
-    return dict(step_sec=sec, tok_s=N / sec)
+        eager = time_events(step, max(steps // 3, 3), stream)
+    log(f"model decode step, eager launches: {eager * 1e3:.3f} ms, {N / eager:.0f} tok/s")
+    # the same step captured once as a HIP graph and replayed
+    from serving.graph_step import DecodeStepGraph
+    graph = DecodeStepGraph(model, pool, meta, ids, warmup=1)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    sec = time_events(graph.replay, steps, stream)
+    log(f"model decode step, HIP graph: {sec * 1e3:.3f} ms, {N / sec:.0f} tok/s")
+    return dict(step_sec=sec, tok_s=N / sec, eager_step_sec=eager)
 
 
 def run_north_star(args, torch):
@@ -241,6 +253,54 @@ def run_cpu_baseline(hot, torch):
                       "(oracle/torch_ref.paged_attention_sdpa)"}
 
 
+def run_profile(args, torch):
+    """Profiling target: only the decode-attention launches of one workload
+    (no timing, no JSON), optionally followed by a plain device copy of
+    known size, the reference for scaling HBM counters."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_attention_meta, paged_mqa_decode
+    from serving.kv_pool import KVPool
+    from serving.paged_meta import pack_batch_meta
+
+    dev = torch.device("cuda:0")
+    if args.profile == "cfg4":
+        L, N, HQ, HKV, D, BS, NB = 1, 128, 16, 1, 64, 16, 16384
+        lens = workloads.lengths_uniform(N, 256, 2048, seed=0)
+        tables = cfg4_tables(lens, BS, NB, 1, seed=0)
+        pool = KVPool(L, BS, NB, HKV, D, torch.bfloat16, dev)
+        g = torch.Generator(device=dev).manual_seed(0)
+        pool.kv[0].normal_(generator=g)
+        meta = pack_batch_meta(tables, list(range(N + 1)), [int(x) for x in lens], N, dev, BS)
+        q = torch.randn(N, HQ, D, generator=g, device=dev).bfloat16()
+        out = torch.empty_like(q)
+
+        def attn():
+            paged_attention_meta(q, pool.kv[0, 0], pool.kv[0, 1], meta, out=out)
+        nbytes = attn_bytes(lens + 1, HQ, HKV, D, 2, BS)
+    else:
+        p = workloads.cfg5_problem(dev, seed=0, bs=16)
+        out = torch.empty_like(p.q)
+        mk = int(p.lens.max())
+
+        def attn():
+            paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens,
+                             max_kv_len=mk, out=out)
+        nbytes = attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs)
+    for _ in range(args.profile_iters):
+        attn()
+    torch.cuda.synchronize()
+    if args.copy_mib > 0:
+        # an elementwise kernel (a same-dtype copy_ would be a DMA transfer,
+        # invisible to kernel counters): reads and writes copy_mib MiB
+        src = torch.ones(args.copy_mib << 19, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+    log(f"profile {args.profile}: {args.profile_iters} attention launches of "
+        f"{nbytes} algorithmic bytes; copy {args.copy_mib} MiB x 3")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,6 +310,12 @@ def main():
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
+    ap.add_argument("--profile", choices=["cfg4", "cfg5"], default=None,
+                    help="run only the decode-attention launches of this workload "
+                         "(a rocprofv3 target); no JSON line")
+    ap.add_argument("--profile-iters", type=int, default=20)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="with --profile: also copy this many MiB device to device, 3 times")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -264,6 +330,9 @@ def main():
         sys.exit(2)
     from serving import _native
     _native.lib()
+    if args.profile:
+        run_profile(args, torch)
+        return
 
     hot = run_hot_path(args, torch)
     value = hot["step_bytes"] / hot["step_sec"] / 1e9
@@ -272,11 +341,18 @@ def main():
     cpu = None if args.no_cpu else run_cpu_baseline(hot, torch)
 
     achieved = hot["attn_bytes"] / hot["attn_sec"] / 1e9
-    traffic = None
-    tpath = os.path.join(REPO, "profiles", "traffic_cfg4_attention.json")
-    if os.path.exists(tpath):
+
+    def traffic_of(w):
+        # HBM bytes per attention op from the committed rocprofv3 counter
+        # summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size)
+        tpath = os.path.join(REPO, "profiles", f"traffic_{w}_attention.json")
+        if not os.path.exists(tpath):
+            return None
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            return json.load(f).get("hbm_bytes_per_launch")
+    traffic = traffic_of("cfg4")
+    if ns is not None:
+        ns["traffic"] = traffic_of("cfg5")
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -302,8 +378,12 @@ def main():
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tok_s": None if model is None else round(model["tok_s"], 1),
         "decode_step_ms": None if model is None else round(model["step_sec"] * 1e3, 4),
+        "decode_step": "the whole greedy decode step (12 layers + argmax + metadata advance) "
+                       "replayed from one HIP graph",
+        "decode_tok_s_eager": None if model is None else round(N_MODEL / model["eager_step_sec"], 1),
         "roofline": {
-            "kernel": "paged MQA decode attention (cfg4, one layer)",
+            "kernel": "paged MQA decode attention, cfg4, one layer: decode_mfma_kernel + "
+                      "split-K merge_kernel (one launch pair, timed together)",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
