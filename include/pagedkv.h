@@ -30,6 +30,8 @@
  *                         (paged_attn_fwd_cuda      kernels/pagedattn/pagedattn.cu:1052-1079)
  *   pkv_attention_workspace_bytes  no counterpart: the reference kernel has no
  *                         split-K and therefore no workspace.
+ *   pkv_paged_attention_append  KVPool.write + paged_varlen_attention per
+ *                         layer                      serving/paged_mqa.py:98-110
  */
 #ifndef PAGEDKV_H
 #define PAGEDKV_H
@@ -159,6 +161,33 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
                         float scale, int causal, int part_tokens, int dtype,
                         void* workspace, size_t workspace_bytes, int* status,
                         void* stream);
+
+/*
+ * pkv_append_from_table followed by pkv_paged_attention in one call: the
+ * step's new K/V rows (k_new, v_new [n_tokens, hkv, d], row t of sequence s
+ * at position start_pos[s] + t - query_start_loc[s]) are appended to the
+ * pools and attended to by the same launch. On the MFMA decode kernels
+ * (bf16/f16, one query per sequence, 16 or 32 query heads per kv head,
+ * d = 64 or 128) the append is fused into the attention: the workgroup
+ * whose context range covers the new row takes it from k_new / v_new and
+ * the one holding the sequence's last chunk writes it to its pool slot;
+ * elsewhere the two steps run back to back. Same results, status bits
+ * and pool contents as the two calls. query_start_loc is required.
+ * Replaces KVPool.write + paged_varlen_attention as called per layer in
+ * MQA_Paged.forward_paged_batched (serving/paged_mqa.py:98-110).
+ */
+int pkv_paged_attention_append(void* out, float* lse, const void* q,
+                               void* k_pool, void* v_pool,
+                               int64_t num_blocks, int block_size,
+                               const int32_t* block_tables, int max_blk,
+                               const int32_t* seq_lens,
+                               const int32_t* query_start_loc, int n_seq,
+                               int n_tokens, int max_q_len, int max_kv_len,
+                               int hq, int hkv, int d, float scale, int causal,
+                               int part_tokens, int dtype, const void* k_new,
+                               const void* v_new, const int32_t* start_pos,
+                               void* workspace, size_t workspace_bytes,
+                               int* status, void* stream);
 
 #ifdef __cplusplus
 }

@@ -129,17 +129,20 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
       .ws_bytes;
 }
 
-int pkv_paged_attention(void* out, float* lse, const void* q,
-                        const void* k_pool, const void* v_pool,
-                        int64_t num_blocks, int block_size,
-                        const int32_t* block_tables, int max_blk,
-                        const int32_t* seq_lens,
-                        const int32_t* query_start_loc, int n_seq,
-                        int n_tokens, int max_q_len, int max_kv_len, int hq,
-                        int hkv, int d,
-                        float scale, int causal, int part_tokens, int dtype,
-                        void* workspace, size_t workspace_bytes, int* status,
-                        void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Shared body of pkv_paged_attention (k_new == NULL) and
+// pkv_paged_attention_append.
+int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
+                   const void* v_pool, int64_t num_blocks, int block_size,
+                   const int32_t* block_tables, int max_blk, const int32_t* seq_lens,
+                   const int32_t* query_start_loc, int n_seq, int n_tokens, int max_q_len,
+                   int max_kv_len, int hq, int hkv, int d, float scale, int causal,
+                   int part_tokens, int dtype, void* workspace, size_t workspace_bytes,
+                   int* status, void* stream, const void* k_new, const void* v_new,
+                   const int32_t* start_pos) {
   g_err[0] = 0;
   if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
   if (hkv <= 0 || hq <= 0 || hq % hkv != 0)
@@ -198,7 +201,60 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
   a.ws_o = ws;
   a.ws_ml = ws ? ws + units * plan.rows * (size_t)d : nullptr;
   a.status = status;
+  if (k_new) {
+    if (plan.kind == 0) {
+      // no fused form for the generic kernel: append, then attend
+      const int rc = launch_append_from_table(
+          const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
+          v_new, block_tables, max_blk, query_start_loc, start_pos,
+          n_seq, n_tokens, (int64_t)hkv * d * elem_bytes(dtype), status,
+          (hipStream_t)stream);
+      if (rc != PKV_OK) return rc;
+    } else {
+      a.k_new = k_new;
+      a.v_new = v_new;
+      a.new_pos = start_pos;
+    }
+  }
   return launch_attention(a, plan, dtype, (hipStream_t)stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int pkv_paged_attention(void* out, float* lse, const void* q,
+                        const void* k_pool, const void* v_pool,
+                        int64_t num_blocks, int block_size,
+                        const int32_t* block_tables, int max_blk,
+                        const int32_t* seq_lens,
+                        const int32_t* query_start_loc, int n_seq,
+                        int n_tokens, int max_q_len, int max_kv_len, int hq,
+                        int hkv, int d,
+                        float scale, int causal, int part_tokens, int dtype,
+                        void* workspace, size_t workspace_bytes, int* status,
+                        void* stream) {
+  return attention_impl(out, lse, q, k_pool, v_pool, num_blocks, block_size, block_tables,
+                        max_blk, seq_lens, query_start_loc, n_seq, n_tokens, max_q_len,
+                        max_kv_len, hq, hkv, d, scale, causal, part_tokens, dtype, workspace,
+                        workspace_bytes, status, stream, nullptr, nullptr, nullptr);
+}
+
+int pkv_paged_attention_append(void* out, float* lse, const void* q, void* k_pool,
+                               void* v_pool, int64_t num_blocks, int block_size,
+                               const int32_t* block_tables, int max_blk,
+                               const int32_t* seq_lens, const int32_t* query_start_loc,
+                               int n_seq, int n_tokens, int max_q_len, int max_kv_len, int hq,
+                               int hkv, int d, float scale, int causal, int part_tokens,
+                               int dtype, const void* k_new, const void* v_new,
+                               const int32_t* start_pos, void* workspace,
+                               size_t workspace_bytes, int* status, void* stream) {
+  if (n_tokens > 0 && (!k_new || !v_new || !start_pos || !query_start_loc))
+    return fail(PKV_ERR_INVALID, "null k_new / v_new / start_pos / query_start_loc");
+  return attention_impl(out, lse, q, k_pool, v_pool, num_blocks, block_size, block_tables,
+                        max_blk, seq_lens, query_start_loc, n_seq, n_tokens, max_q_len,
+                        max_kv_len, hq, hkv, d, scale, causal, part_tokens, dtype, workspace,
+                        workspace_bytes, status, stream, k_new, v_new, start_pos);
 }
 
 }  // extern "C"

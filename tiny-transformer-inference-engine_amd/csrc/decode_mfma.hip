@@ -80,6 +80,18 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   bool bad_block = false;
   WaveState<NT, DT> st;
   st.reset();
+  // fused append: the partition holding the new row's position stages it
+  // from k_new / v_new; the last partition writes it into the pool
+  __shared__ __attribute__((aligned(16))) char new_lds[2 * Geo::ROW_BYTES];
+  NewRow nr;
+  nr.pos = -1;
+  nr.lds = new_lds;
+  const int new_pos = a.new_pos ? a.new_pos[s] : -1;
+  const bool new_here = a.new_pos && new_pos >= kv_lo && new_pos < kv_hi;
+  const bool new_write = a.new_pos && part == g.nparts - 1;
+  if (new_here) nr.pos = new_pos;
+  bool new_pending = new_here || new_write;  // row buffer still to fill
+  int last_blk_lo = 0, last_nblk = 0;
 
   // walk the partition in windows of kTblCap - 1 blocks of tokens, so that a
   // window starting inside a block still touches at most kTblCap table
@@ -91,11 +103,27 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     cx.blk_lo = lo >> a.bs_shift;
     const int nblk = ((cx.seg_hi - 1) >> a.bs_shift) + 1 - cx.blk_lo;
     __syncthreads();  // previous window's table no longer read
-    for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+    if (new_pending) {
+      // the new row's load is in flight with the table slice's
+      const u32x4 piece = load_new_row<D>(a, g.q_begin, kvh, threadIdx.x);
+      for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+      put_new_row<D>(new_lds, piece, threadIdx.x);
+      new_pending = false;
+    } else {
+      for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+    }
     __syncthreads();
-    run_chunks<T, D, NT, PF, OFF64>(w, kWaves, cx, pv, qf, st, bad_block);
+    run_chunks<T, D, NT, PF, OFF64>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+    last_blk_lo = cx.blk_lo;
+    last_nblk = nblk;
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
+  if (new_write) {
+    if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, g.q_begin, kvh, threadIdx.x),
+                                    threadIdx.x);
+    // each thread stores the piece it put into the buffer itself
+    store_new_row<D>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk, threadIdx.x);
+  }
 
   // ---- merge the 4 wavefronts' partial states through LDS ----
 #pragma unroll

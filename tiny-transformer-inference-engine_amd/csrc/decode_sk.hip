@@ -101,6 +101,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   __shared__ int tbl[kTblCap];
   __shared__ int scan_sh[kBlock];
   __shared__ int s_v0, s_g0;
+  __shared__ __attribute__((aligned(16))) char new_lds[2 * Geo::ROW_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -200,6 +201,18 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
 
     v8 qf[NT][D / 32];
     load_q<T, D, NT>(qf, q, qrow0, grp, l16);
+    // fused append: this share stages the new row when it covers its
+    // position, and writes it into the pool when it holds the last chunk
+    NewRow nr;
+    nr.pos = -1;
+    nr.lds = new_lds;
+    const int new_pos = a.new_pos ? a.new_pos[s] : -1;
+    const bool new_here = a.new_pos && new_pos >= tok_lo && new_pos < tok_hi;
+    const bool new_write = a.new_pos && c1 == n;
+    if (new_here) nr.pos = new_pos;
+    bool new_pending = new_here || new_write;  // row buffer still to fill
+    const int new_tok = (int)(qrow0 / a.hq);
+    int last_blk_lo = 0, last_nblk = 0;
     pv.head_off = (int64_t)kvh * D * 2;
     const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
     WaveState<NT, DT> st;
@@ -209,10 +222,25 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       cx.seg_hi = min(lo + win, tok_hi);
       cx.blk_lo = lo >> a.bs_shift;
       const int nblk = ((cx.seg_hi - 1) >> a.bs_shift) + 1 - cx.blk_lo;
-      __syncthreads();  // previous window's table / slices no longer read
-      for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+      __syncthreads();  // previous window's table / slices / row buffer no longer read
+      if (new_pending) {
+        // the new row's load is in flight with the table slice's
+        const u32x4 piece = load_new_row<D>(a, new_tok, kvh, tid);
+        for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+        put_new_row<D>(new_lds, piece, tid);
+        new_pending = false;
+      } else {
+        for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+      }
       __syncthreads();
-      run_chunks<T, D, NT, PF, OFF64>(w, kWaves, cx, pv, qf, st, bad_block);
+      run_chunks<T, D, NT, PF, OFF64>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+      last_blk_lo = cx.blk_lo;
+      last_nblk = nblk;
+    }
+    if (new_write) {
+      if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, new_tok, kvh, tid), tid);
+      // each thread stores the piece it put into the buffer itself
+      store_new_row<D>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk, tid);
     }
 
     // ---- merge the wavefronts' states through LDS ----

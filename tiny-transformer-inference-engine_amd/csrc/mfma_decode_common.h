@@ -158,6 +158,30 @@ struct WaveState {
   }
 };
 
+// The row appended this step (fused append): token position `pos` (-1: none
+// in this range), its K and V rows staged in LDS at lds (K: ROW_BYTES bytes,
+// then V).
+struct NewRow {
+  int pos;
+  const char* lds;
+};
+
+// Overwrites the staged row of token nr.pos when it lies in the chunk that
+// starts at token cb (its pool row may not be written yet).
+template <class Geo>
+__device__ __forceinline__ void stage_new_row(const NewRow& nr, int cb, const ChunkCtx& cx,
+                                              int lane) {
+  if (nr.pos >= cb && nr.pos < cb + kChunk) {  // uniform across the wavefront
+    const int r = nr.pos - cb;
+    if (lane < 2 * Geo::CPR) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(nr.lds + lane * 16);
+      char* dst = lane < Geo::CPR ? cx.kl + Geo::off(r, lane)
+                                  : cx.vl + Geo::off(r, lane - Geo::CPR);
+      *reinterpret_cast<u32x4*>(dst) = x;
+    }
+  }
+}
+
 // Registers -> this wavefront's LDS slice (rows with a bad table entry are
 // zeroed and flagged).
 template <class Geo, int NPL>
@@ -298,9 +322,10 @@ template <typename T, int D, int NT, int NPL, bool OFF64>
 __device__ __forceinline__ void chunk_step(
     ChunkRegs<NPL>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
     const PoolView& pv, const typename Ops<T>::v8 (&qf)[NT][D / 32],
-    WaveState<NT, D / 16>& st, bool& bad_block) {
+    WaveState<NT, D / 16>& st, bool& bad_block, const NewRow& nr) {
   using Geo = ChunkGeo<D>;
   stage_chunk<Geo, NPL>(r, cx, bad_block);
+  stage_new_row<Geo>(nr, cx.seg_lo + c * kChunk, cx, (int)(threadIdx.x & 63));
   if (refill) load_chunk<Geo, NPL, OFF64>(r, pv, cx, c + ahead);
   compute_chunk<T, D, NT>(c, cx, qf, st);
 }
@@ -313,7 +338,8 @@ template <typename T, int D, int NT, int PF, bool OFF64>
 __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
                                            const PoolView& pv,
                                            const typename Ops<T>::v8 (&qf)[NT][D / 32],
-                                           WaveState<NT, D / 16>& st, bool& bad_block) {
+                                           WaveState<NT, D / 16>& st, bool& bad_block,
+                                           const NewRow& nr) {
   using Geo = ChunkGeo<D>;
   constexpr int NPL = Geo::NPL;
   const int nchunks = (cx.seg_hi - cx.seg_lo + kChunk - 1) / kChunk;
@@ -327,19 +353,69 @@ __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
 #pragma unroll
     for (int b = 0; b < PF; ++b)
       chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, true, step, cx, pv, qf, st,
-                                       bad_block);
+                                       bad_block, nr);
   }
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
       chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, c + nw * (b + PF) < nchunks, step,
-                                       cx, pv, qf, st, bad_block);
+                                       cx, pv, qf, st, bad_block, nr);
   c += step;
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
       chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, false, step, cx, pv, qf, st,
-                                       bad_block);
+                                       bad_block, nr);
+}
+
+// Fused append of one sequence's query-token row. load_new_row /
+// put_new_row: threads [0, 2 CPR) of the workgroup copy their 16-byte piece
+// of the K / V row `tok` (kv head `kvh`) into the LDS row buffer (the
+// caller's barrier publishes it). store_new_row: the same threads write it
+// into the pool slot of
+// position pos, after the table and pool checks of the stand-alone append
+// (whose status bits are raised instead of writing); the table entry comes
+// from the LDS table window tbl (blocks blk_lo ...) when it covers pos.
+// Every thread loads a piece (threads past 2 CPR a duplicate, so no load
+// sits under a branch); put_new_row then stores threads [0, 2 CPR)'s pieces.
+template <int D>
+__device__ __forceinline__ u32x4 load_new_row(const AttnArgs& a, int tok, int kvh, int tid) {
+  using Geo = ChunkGeo<D>;
+  const int t = tid % (2 * Geo::CPR);
+  const bool is_v = t >= Geo::CPR;
+  const int64_t off = ((int64_t)tok * a.hkv + kvh) * D * 2 + (t % Geo::CPR) * 16;
+  return *reinterpret_cast<const u32x4*>(static_cast<const char*>(is_v ? a.v_new : a.k_new) +
+                                         off);
+}
+
+template <int D>
+__device__ __forceinline__ void put_new_row(char* lds, u32x4 piece, int tid) {
+  if (tid < 2 * ChunkGeo<D>::CPR) *reinterpret_cast<u32x4*>(lds + tid * 16) = piece;
+}
+
+template <int D>
+__device__ __forceinline__ void store_new_row(const char* lds, const AttnArgs& a, int s,
+                                              int kvh, int pos, const int* tbl, int blk_lo,
+                                              int nblk, int tid) {
+  using Geo = ChunkGeo<D>;
+  if (tid >= 2 * Geo::CPR) return;
+  const int page = pos >> a.bs_shift;
+  if (pos < 0 || page >= a.max_blk) {
+    if (a.status && tid == 0) atomicOr(a.status, PKV_STATUS_SHORT_TABLE);
+    return;
+  }
+  const int64_t phys = page >= blk_lo && page < blk_lo + nblk
+                           ? tbl[page - blk_lo]
+                           : a.block_tables[(int64_t)s * a.max_blk + page];
+  if (phys <= 0 || phys >= a.num_blocks) {
+    if (a.status && tid == 0) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
+    return;
+  }
+  const bool is_v = tid >= Geo::CPR;
+  const int64_t slot = (phys << a.bs_shift) + (pos & ((1 << a.bs_shift) - 1));
+  char* pool = static_cast<char*>(const_cast<void*>(is_v ? a.v_pool : a.k_pool));
+  *reinterpret_cast<u32x4*>(pool + (slot * a.hkv + kvh) * D * 2 + (tid % Geo::CPR) * 16) =
+      *reinterpret_cast<const u32x4*>(lds + tid * 16);
 }
 
 // Q^T fragments of one (token, kv head): head 16*nt + l16, dims of piece

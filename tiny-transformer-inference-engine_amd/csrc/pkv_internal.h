@@ -73,6 +73,12 @@ struct AttnArgs {
   float* ws_o;       // [units][ROWS][d] unnormalised partial outputs
   float* ws_ml;      // [units][ROWS][2] (running max (log2 units), sum)
   int* status;
+  // fused append (decode MFMA kernels; all null otherwise): the K/V row of
+  // sequence s's query token goes to position new_pos[s] of its table, and
+  // the attention uses it from k_new / v_new
+  const void* k_new;
+  const void* v_new;
+  const int32_t* new_pos;
 };
 
 // Rows ((query token, head) pairs of one kv head) per tile of the generic

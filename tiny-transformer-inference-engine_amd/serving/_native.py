@@ -51,6 +51,11 @@ _SIGNATURES = {
                              _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
                              _c_int, _c_int, _c_vp, _c_size, _c_vp, _c_vp],
                             _c_int),
+    "pkv_paged_attention_append": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int,
+                                    _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int,
+                                    _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
+                                    _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_size,
+                                    _c_vp, _c_vp], _c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

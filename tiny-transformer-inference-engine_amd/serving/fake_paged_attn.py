@@ -214,6 +214,45 @@ def paged_attention_meta(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Te
     return out
 
 
+def paged_attention_append_meta(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pool,
+                                layer: int, meta: PagedBatchMeta,
+                                scale: Optional[float] = None, causal: bool = True,
+                                out: Optional[torch.Tensor] = None,
+                                lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """pool.write_from_table(layer, k, v, meta) followed by
+    paged_attention_meta(q, ..., meta) in one library call
+    (pkv_paged_attention_append): on the MFMA decode kernels the append is
+    fused into the attention launch. Same pool contents, outputs and errors
+    as the two calls (serving/paged_mqa.py:98-110)."""
+    pool.check_rows(k, v, meta)
+    _native.require_device(q, k, v, pool.kv, what="paged_attention_append_meta")
+    if out is None:
+        out = torch.empty_like(q)
+    k = k.contiguous()
+    v = v.contiguous()
+    T, hq, d = q.shape
+    kp, vp = pool.flat_k[layer], pool.flat_v[layer]
+    code = _native.dtype_code(q.dtype)
+    L = _native.lib()
+    max_blk = meta.block_tables.shape[1] if meta.block_tables.dim() == 2 else 0
+    ws_bytes = L.pkv_attention_workspace_bytes(
+        meta.num_seqs, meta.max_q_len, hq, pool.num_kv_heads, d, max_blk, pool.block_size,
+        meta.max_kv_len, 0, code)
+    ws = _native.WORKSPACE.get(q.device, ws_bytes)
+    status = pool._status()
+    rc = L.pkv_paged_attention_append(
+        out.data_ptr(), _native.ptr(lse), q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+        pool.num_blocks, pool.block_size, meta.block_tables.data_ptr() if max_blk else None,
+        max_blk, meta.seq_lens.data_ptr(), meta.query_start_loc.data_ptr(), meta.num_seqs, T,
+        meta.max_q_len, meta.max_kv_len, hq, pool.num_kv_heads, d,
+        float(scale if scale is not None and scale > 0 else 0.0), int(bool(causal)), 0, code,
+        k.data_ptr(), v.data_ptr(), meta.start_pos.data_ptr(), _native.ptr(ws), ws_bytes,
+        _native.ptr(status), _native.stream_ptr(q.device))
+    _native.check(rc, "pkv_paged_attention_append")
+    pool._raise_status(status, "paged_attention_append_meta")
+    return out
+
+
 def paged_mqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                      block_tables: torch.Tensor, seq_lens: torch.Tensor,
                      scale: Optional[float] = None, max_kv_len: int = 0,

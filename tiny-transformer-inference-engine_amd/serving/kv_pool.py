@@ -135,10 +135,8 @@ class KVPool:
         _native.check(rc, "pkv_append")
         self._raise_status(status, "KVPool.write")
 
-    def write_from_table(self, layer: int, k: torch.Tensor, v: torch.Tensor, meta) -> None:
-        """Append the step's new K/V rows of every sequence with slots computed
-        in-kernel from `meta` (a PagedBatchMeta): equivalent to
-        make_slot_mapping per sequence + one write (serving/paged_mqa.py:87-99)."""
+    def check_rows(self, k: torch.Tensor, v: torch.Tensor, meta) -> None:
+        """The checks of KVPool.write (kv_pool.py:58-67) for a step's rows."""
         assert k.shape == v.shape, f"k/v shape mismatch: {k.shape} vs {v.shape}"
         assert k.shape[1:] == (self.num_kv_heads, self.head_dim), \
             f"k trailing dims {k.shape[1:]} != expected {(self.num_kv_heads, self.head_dim)}"
@@ -146,6 +144,12 @@ class KVPool:
             f"k/v dtype {k.dtype}/{v.dtype} != pool dtype {self.dtype}"
         assert k.shape[0] == meta.num_tokens, \
             f"k has {k.shape[0]} rows but the batch has {meta.num_tokens} tokens"
+
+    def write_from_table(self, layer: int, k: torch.Tensor, v: torch.Tensor, meta) -> None:
+        """Append the step's new K/V rows of every sequence with slots computed
+        in-kernel from `meta` (a PagedBatchMeta): equivalent to
+        make_slot_mapping per sequence + one write (serving/paged_mqa.py:87-99)."""
+        self.check_rows(k, v, meta)
         _native.require_device(self.kv, k, v, what="KVPool.write_from_table")
         k = k.contiguous()
         v = v.contiguous()

@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from .fake_paged_attn import paged_attention_meta
+from .fake_paged_attn import paged_attention_append_meta, paged_attention_meta
 from .layers import RoPE
 from .paged_meta import PagedBatchMeta, pack_batch_meta
 
@@ -93,7 +93,6 @@ class MQA_Paged(nn.Module):
         v = self.v_proj(x).view(T, self.num_kv_heads, self.headdim)
         q, k = self.rope.forward_tokens(q, k, meta.positions)
 
-        pool.write_from_table(layer_idx, k, v, meta)
-        k_pool, v_pool = _get_kv_pool(pool, layer_idx)
-        out = paged_attention_meta(q.contiguous(), k_pool, v_pool, meta)
+        # append + attention in one library call (fused on the decode kernels)
+        out = paged_attention_append_meta(q.contiguous(), k, v, pool, layer_idx, meta)
         return self.out(out.view(T, d_model))
