@@ -8,8 +8,10 @@ head_dim 64, context lengths U[256, 2048] (seed 0), block_size 16, a
 16384-block pool per layer, tables a random permutation of pool blocks.
 One STEP is the path's work for one decode step of that batch: for each of
 the 12 layers, the slot-mapped append of the 128 new K/V rows and the paged
-MQA decode attention over the layer's pool. K/V, Q and metadata are resident
-in HBM before timing starts.
+MQA decode attention over the layer's pool, issued as one library call per
+layer (pkv_paged_attention_append); the same work as two calls per layer is
+reported as value_two_calls. K/V, Q and metadata are resident in HBM before
+timing starts.
 
 Printed JSON line:
   value        algorithmic HBM bytes of the timed steps / their wall time
@@ -83,9 +85,13 @@ def cfg4_tables(lens, bs, num_blocks, extra_tokens, seed):
 
 
 def run_hot_path(args, torch):
-    """Config-4 hot path: 12 x (append + paged decode attention)."""
+    """Config-4 hot path: 12 x (append + paged decode attention), one
+    library call per layer (pkv_paged_attention_append: the append fused
+    into the attention launch). The same step as two calls per layer
+    (KVPool.write_from_table + paged_attention_meta, the reference's
+    serving/paged_mqa.py:98-110 structure) is timed beside it."""
     from serving import workloads
-    from serving.fake_paged_attn import paged_attention_meta
+    from serving.fake_paged_attn import paged_attention_append_meta, paged_attention_meta
     from serving.kv_pool import KVPool
     from serving.paged_meta import pack_batch_meta
 
@@ -109,6 +115,10 @@ def run_hot_path(args, torch):
 
     def step():
         for l in range(L):
+            paged_attention_append_meta(q, knew, vnew, pool, l, meta, out=out)
+
+    def step_two_calls():
+        for l in range(L):
             pool.write_from_table(l, knew, vnew, meta)
             paged_attention_meta(q, pool.kv[l, 0], pool.kv[l, 1], meta, out=out)
 
@@ -125,6 +135,10 @@ def run_hot_path(args, torch):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
     log(f"hot path: {sec * 1e6:.1f} us/step (events), {wall * 1e6:.1f} us/step (wall)")
+    for _ in range(args.warmup):
+        step_two_calls()
+    sec2 = time_events(step_two_calls, args.steps, stream)
+    log(f"hot path as append + attention calls: {sec2 * 1e6:.1f} us/step")
 
     # the dominant kernel alone: attention on layer 0, back to back
     def attn():
@@ -133,7 +147,7 @@ def run_hot_path(args, torch):
         attn()
     a_sec = time_events(attn, 200, stream)
     log(f"attention alone: {a_sec * 1e6:.2f} us/launch, {per_layer_attn / 1e6:.2f} MB")
-    return dict(step_sec=sec, wall_sec=wall, step_bytes=step_bytes,
+    return dict(step_sec=sec, wall_sec=wall, step_bytes=step_bytes, step_sec_two_calls=sec2,
                 attn_sec=a_sec, attn_bytes=per_layer_attn, lens=lens, tables=tables,
                 pool=pool, q=q, meta=meta)
 
@@ -367,8 +381,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "cfg4 paged decode step: 12 layers x (slot-mapped KV append of 128 rows + "
-                        "paged MQA decode attention), batch 128, Hq 16, Hkv 1, D 64, ctx "
+            "workload": "cfg4 paged decode step: 12 layers x (slot-mapped KV append of 128 rows "
+                        "fused into the paged MQA decode attention), batch 128, Hq 16, Hkv 1, D 64, ctx "
                         "U[256,2048] seed 0, block_size 16, 16384-block pool per layer",
             "global_batch": 128,
             "layers": 12,
@@ -376,6 +390,7 @@ def main():
             "parallelism": "none (1 GPU)",
         },
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "value_two_calls": round(hot["step_bytes"] / hot["step_sec_two_calls"] / 1e9, 2),
         "decode_tok_s": None if model is None else round(model["tok_s"], 1),
         "decode_step_ms": None if model is None else round(model["step_sec"] * 1e3, 4),
         "decode_step": "the whole greedy decode step (12 layers + argmax + metadata advance) "

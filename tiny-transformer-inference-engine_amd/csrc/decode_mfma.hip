@@ -26,8 +26,9 @@ constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
 
 // PF = chunks each wavefront keeps in flight in registers; OCC = wavefronts
-// per SIMD the register budget is sized for.
-template <typename T, int D, int NT, int PF, int OCC, bool OFF64>
+// per SIMD the register budget is sized for; APP = the fused append of
+// a.k_new / a.v_new at a.new_pos (compiled out of the plain attention).
+template <typename T, int D, int NT, int PF, int OCC, bool OFF64, bool APP>
 __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -86,11 +87,15 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   NewRow nr;
   nr.pos = -1;
   nr.lds = new_lds;
-  const int new_pos = a.new_pos ? a.new_pos[s] : -1;
-  const bool new_here = a.new_pos && new_pos >= kv_lo && new_pos < kv_hi;
-  const bool new_write = a.new_pos && part == g.nparts - 1;
-  if (new_here) nr.pos = new_pos;
-  bool new_pending = new_here || new_write;  // row buffer still to fill
+  int new_pos = -1;
+  bool new_write = false, new_pending = false;  // pending: row buffer still to fill
+  if constexpr (APP) {
+    new_pos = a.new_pos[s];
+    const bool new_here = new_pos >= kv_lo && new_pos < kv_hi;
+    new_write = part == g.nparts - 1;
+    if (new_here) nr.pos = new_pos;
+    new_pending = new_here || new_write;
+  }
   int last_blk_lo = 0, last_nblk = 0;
 
   // walk the partition in windows of kTblCap - 1 blocks of tokens, so that a
@@ -103,7 +108,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     cx.blk_lo = lo >> a.bs_shift;
     const int nblk = ((cx.seg_hi - 1) >> a.bs_shift) + 1 - cx.blk_lo;
     __syncthreads();  // previous window's table no longer read
-    if (new_pending) {
+    if (APP && new_pending) {
       // the new row's load is in flight with the table slice's
       const u32x4 piece = load_new_row<D>(a, g.q_begin, kvh, threadIdx.x);
       for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
@@ -113,12 +118,12 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
       for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
     }
     __syncthreads();
-    run_chunks<T, D, NT, PF, OFF64>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+    run_chunks<T, D, NT, PF, OFF64, APP>(w, kWaves, cx, pv, qf, st, bad_block, nr);
     last_blk_lo = cx.blk_lo;
     last_nblk = nblk;
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
-  if (new_write) {
+  if (APP && new_write) {
     if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, g.q_begin, kvh, threadIdx.x),
                                     threadIdx.x);
     // each thread stores the piece it put into the buffer itself
@@ -185,20 +190,31 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   }
 }
 
+// <T, D, NT, PF, OCC, OFF64, APP>: two wavefronts per SIMD
+template <typename T, int D, int NT, int PF, bool OFF64>
+void launch_v(const AttnArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.new_pos)
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, true>), grid, dim3(kBlock), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, false>), grid, dim3(kBlock),
+                       0, stream, a);
+}
+
 template <typename T, bool OFF64>
 int launch_t(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
   const dim3 grid(a.n_seq * a.hkv, p.parts_max);
   const int nt = a.group / 16;
-  // <T, D, NT, PF, OCC, OFF64>: two wavefronts per SIMD; the D = 128 variants
-  // have room for one chunk in flight per wavefront, the D = 64 ones for two
+  // the D = 128 variants have room for one chunk in flight per wavefront,
+  // the D = 64 ones for two
   if (a.d == 64 && nt == 1)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, 64, 1, 2, 2, OFF64>), grid, dim3(kBlock), 0, stream, a);
+    launch_v<T, 64, 1, 2, OFF64>(a, grid, stream);
   else if (a.d == 64 && nt == 2)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, 64, 2, 2, 2, OFF64>), grid, dim3(kBlock), 0, stream, a);
+    launch_v<T, 64, 2, 2, OFF64>(a, grid, stream);
   else if (a.d == 128 && nt == 1)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, 128, 1, 1, 2, OFF64>), grid, dim3(kBlock), 0, stream, a);
+    launch_v<T, 128, 1, 1, OFF64>(a, grid, stream);
   else if (a.d == 128 && nt == 2)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, 128, 2, 1, 2, OFF64>), grid, dim3(kBlock), 0, stream, a);
+    launch_v<T, 128, 2, 1, OFF64>(a, grid, stream);
   else
     return fail(PKV_ERR_UNSUPPORTED, "decode_mfma: d=%d group=%d", a.d, a.group);
   return check_launch("decode_mfma_kernel");

@@ -79,13 +79,14 @@ __device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
     __syncthreads();
   }
   const int incl = sh[t];
-  const int total = sh[kBlock - 1];
+  // the same for every thread: keep it scalar
+  const int total = __builtin_amdgcn_readfirstlane(sh[kBlock - 1]);
   __syncthreads();
   excl = incl - x;
   return total;
 }
 
-template <typename T, int D, int NT, int PF, bool OFF64>
+template <typename T, int D, int NT, int PF, bool OFF64, bool APP>
 __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs k) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -178,8 +179,9 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   // touches at most kTblCap table entries
   const int win = (kTblCap - 1) << a.bs_shift;
 
-  int v = s_v0;
-  int g0 = s_g0;  // cost position where sequence v's interval starts
+  // uniform across the workgroup: scalar registers for the segment loop
+  int v = __builtin_amdgcn_readfirstlane(s_v0);
+  int g0 = __builtin_amdgcn_readfirstlane(s_g0);  // cost position where v's interval starts
   bool first = true;
   // sequence v's chunks sit at units [g0 + K, g0 + K + n); the share's
   // chunks are those among [start, end)
@@ -206,11 +208,15 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     NewRow nr;
     nr.pos = -1;
     nr.lds = new_lds;
-    const int new_pos = a.new_pos ? a.new_pos[s] : -1;
-    const bool new_here = a.new_pos && new_pos >= tok_lo && new_pos < tok_hi;
-    const bool new_write = a.new_pos && c1 == n;
-    if (new_here) nr.pos = new_pos;
-    bool new_pending = new_here || new_write;  // row buffer still to fill
+    int new_pos = -1;
+    bool new_write = false, new_pending = false;  // pending: row buffer still to fill
+    if constexpr (APP) {
+      new_pos = a.new_pos[s];
+      const bool new_here = new_pos >= tok_lo && new_pos < tok_hi;
+      new_write = c1 == n;
+      if (new_here) nr.pos = new_pos;
+      new_pending = new_here || new_write;
+    }
     const int new_tok = (int)(qrow0 / a.hq);
     int last_blk_lo = 0, last_nblk = 0;
     pv.head_off = (int64_t)kvh * D * 2;
@@ -223,7 +229,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       cx.blk_lo = lo >> a.bs_shift;
       const int nblk = ((cx.seg_hi - 1) >> a.bs_shift) + 1 - cx.blk_lo;
       __syncthreads();  // previous window's table / slices / row buffer no longer read
-      if (new_pending) {
+      if (APP && new_pending) {
         // the new row's load is in flight with the table slice's
         const u32x4 piece = load_new_row<D>(a, new_tok, kvh, tid);
         for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
@@ -233,11 +239,11 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
         for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
       }
       __syncthreads();
-      run_chunks<T, D, NT, PF, OFF64>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+      run_chunks<T, D, NT, PF, OFF64, APP>(w, kWaves, cx, pv, qf, st, bad_block, nr);
       last_blk_lo = cx.blk_lo;
       last_nblk = nblk;
     }
-    if (new_write) {
+    if (APP && new_write) {
       if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, new_tok, kvh, tid), tid);
       // each thread stores the piece it put into the buffer itself
       store_new_row<D>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk, tid);
@@ -376,8 +382,12 @@ __global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArg
 template <typename T, int D, int NT, int PF, bool OFF64>
 int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
   k.n_wg = sk_workgroups(D, 16 * NT);
-  hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64>), dim3(k.n_wg), dim3(kBlock), 0,
-                     stream, a, k);
+  if (a.new_pos)
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, true>), dim3(k.n_wg), dim3(kBlock),
+                       0, stream, a, k);
+  else
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, false>), dim3(k.n_wg),
+                       dim3(kBlock), 0, stream, a, k);
   int rc = check_launch("decode_sk_kernel");
   if (rc != PKV_OK) return rc;
   constexpr int G = 16 * NT;
@@ -389,7 +399,8 @@ int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
 template <typename T, bool OFF64>
 int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
   const int nt = a.group / 16;
-  // <T, D, NT, PF, OFF64>: two wavefronts per SIMD; the D = 128 variants
+  // <T, D, NT, PF, OFF64>: two wavefronts per SIMD, with and without the
+  // fused append (APP); the D = 128 variants
   // have room for one chunk in flight per wavefront, the D = 64 ones for two
   if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, OFF64>(a, k, stream);
   if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, OFF64>(a, k, stream);

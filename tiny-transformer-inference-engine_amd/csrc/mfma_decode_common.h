@@ -318,23 +318,24 @@ __device__ __forceinline__ void compute_chunk(int c, const ChunkCtx& cx,
 // One chunk: registers -> LDS slice, optionally refill the registers with
 // chunk `c + ahead` (issued before any compute so the loads overlap it),
 // then QK / softmax / PV out of LDS.
-template <typename T, int D, int NT, int NPL, bool OFF64>
+template <typename T, int D, int NT, int NPL, bool OFF64, bool APP>
 __device__ __forceinline__ void chunk_step(
     ChunkRegs<NPL>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
     const PoolView& pv, const typename Ops<T>::v8 (&qf)[NT][D / 32],
     WaveState<NT, D / 16>& st, bool& bad_block, const NewRow& nr) {
   using Geo = ChunkGeo<D>;
   stage_chunk<Geo, NPL>(r, cx, bad_block);
-  stage_new_row<Geo>(nr, cx.seg_lo + c * kChunk, cx, (int)(threadIdx.x & 63));
+  if constexpr (APP) stage_new_row<Geo>(nr, cx.seg_lo + c * kChunk, cx, (int)(threadIdx.x & 63));
   if (refill) load_chunk<Geo, NPL, OFF64>(r, pv, cx, c + ahead);
   compute_chunk<T, D, NT>(c, cx, qf, st);
 }
 
 // All chunks of [cx.seg_lo, cx.seg_hi) assigned to wavefront w of nw:
-// chunks w, w + nw, ... with PF chunks in flight per wavefront. A
+// chunks w, w + nw, ... with PF chunks in flight per wavefront (APP: the
+// appended row nr is staged over its pool row where it falls). A
 // steady-state loop with no data-dependent branch keeps the compiler's wait
 // counts exact (staging buffer b waits only for buffer b's loads).
-template <typename T, int D, int NT, int PF, bool OFF64>
+template <typename T, int D, int NT, int PF, bool OFF64, bool APP>
 __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
                                            const PoolView& pv,
                                            const typename Ops<T>::v8 (&qf)[NT][D / 32],
@@ -352,19 +353,19 @@ __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
   for (; c + nw * (2 * PF - 1) < nchunks; c += step) {
 #pragma unroll
     for (int b = 0; b < PF; ++b)
-      chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, true, step, cx, pv, qf, st,
+      chunk_step<T, D, NT, NPL, OFF64, APP>(rb[b], c + nw * b, true, step, cx, pv, qf, st,
                                        bad_block, nr);
   }
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
-      chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, c + nw * (b + PF) < nchunks, step,
+      chunk_step<T, D, NT, NPL, OFF64, APP>(rb[b], c + nw * b, c + nw * (b + PF) < nchunks, step,
                                        cx, pv, qf, st, bad_block, nr);
   c += step;
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
-      chunk_step<T, D, NT, NPL, OFF64>(rb[b], c + nw * b, false, step, cx, pv, qf, st,
+      chunk_step<T, D, NT, NPL, OFF64, APP>(rb[b], c + nw * b, false, step, cx, pv, qf, st,
                                        bad_block, nr);
 }
 
