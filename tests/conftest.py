@@ -1,6 +1,9 @@
-"""Test configuration: registers the `gpu` marker and puts the package
+"""Test configuration: registers the `gpu` marker, puts the package
 directory (which holds the drop-in `serving` package) and the repo root
-(for `oracle`) on sys.path."""
+(for `oracle`) on sys.path, and serves the committed fixtures of
+tests/golden/ (`kats`: the reference's known-answer vectors;
+`attention_golden`: small paged-attention problems with textbook outputs)."""
+import json
 import os
 import sys
 
@@ -11,6 +14,30 @@ PKG = os.path.join(REPO, "tiny-transformer-inference-engine_amd")
 for p in (PKG, REPO):
     if p not in sys.path:
         sys.path.insert(0, p)
+
+
+GOLDEN = os.path.join(REPO, "tests", "golden")
+
+
+@pytest.fixture(scope="session")
+def kats():
+    with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="session")
+def attention_golden():
+    """{case: {q, k_pool, v_pool, block_table, seq_lens, query_start_loc,
+    out, lse, hq, hkv, d, bs, max_q_len}} with float64 / int32 arrays."""
+    import numpy as np
+    raw = np.load(os.path.join(GOLDEN, "attention_small.npz"))
+    cases = {}
+    for key in raw.files:
+        case, field = key.split("/")
+        cases.setdefault(case, {})[field] = raw[key]
+    for c in cases.values():
+        c["hq"], c["hkv"], c["d"], c["bs"], c["max_q_len"] = (int(x) for x in c.pop("shape"))
+    return cases
 
 
 def pytest_configure(config):

@@ -50,6 +50,50 @@ def close(out, expect, dtype, what):
 
 
 # ---------------------------------------------------------------------------
+# committed fixture: textbook outputs (tests/golden/attention_small.npz)
+# ---------------------------------------------------------------------------
+
+def _golden_inputs(c, dtype):
+    t = lambda a: torch.from_numpy(a).to(DEV, dtype)  # noqa: E731
+    i = lambda a: torch.from_numpy(a).to(DEV)  # noqa: E731
+    return (t(c["q"]), t(c["k_pool"]), t(c["v_pool"]), i(c["block_table"]), i(c["seq_lens"]),
+            i(c["query_start_loc"]))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_golden_fixture(attention_golden, dtype):
+    # the inputs are bf16-representable, so every dtype sees them exactly
+    for name, c in attention_golden.items():
+        print(f"[golden] {name} {dtype}", flush=True)
+        q, kp, vp, table, lens, qsl = _golden_inputs(c, dtype)
+        O, L = paged_attn_fwd(q, kp, vp, table, lens, qsl, c["max_q_len"])
+        torch.cuda.synchronize()
+        close(O, c["out"], dtype, f"{name} out")
+        Ln = L.cpu().numpy().astype(np.float64)
+        fin = np.isfinite(c["lse"])
+        assert np.array_equal(np.isfinite(Ln), fin), f"{name}: lse +inf rows differ"
+        tol = TOL[dtype]
+        np.testing.assert_allclose(Ln[fin], c["lse"][fin], rtol=tol["rtol"], atol=tol["atol"],
+                                   err_msg=name)
+
+
+@pytest.mark.parametrize("part_tokens", [0, 32, -1], ids=["auto", "plen32", "persistent"])
+def test_golden_fixture_decode_kernels(attention_golden, part_tokens):
+    # the MFMA decode kernels (split-K partition and persistent) on the
+    # fixture's decode cases, bf16
+    for name, c in attention_golden.items():
+        if c["max_q_len"] != 1:
+            continue
+        print(f"[golden decode] {name} part_tokens={part_tokens}", flush=True)
+        q, kp, vp, table, lens, _ = _golden_inputs(c, torch.bfloat16)
+        lse = torch.empty(q.shape[0], q.shape[1], device=DEV)
+        out = paged_mqa_decode(q, kp, vp, table, lens, lse=lse, part_tokens=part_tokens)
+        torch.cuda.synchronize()
+        close(out, c["out"], torch.bfloat16, f"{name} out")
+        np.testing.assert_allclose(lse.cpu().numpy(), c["lse"], rtol=0, atol=2e-2, err_msg=name)
+
+
+# ---------------------------------------------------------------------------
 # isolated paged MQA decode op
 # ---------------------------------------------------------------------------
 

@@ -60,18 +60,20 @@ def test_failed_free_changes_nothing():
     assert a.num_free == before
 
 
-def test_allocation_order_is_ascending_then_lifo():
-    a = BlockAllocator(6)
-    assert a.allocate_n(3) == [1, 2, 3]
-    a.free([2, 1])
-    assert a.allocate() == 1 and a.allocate() == 2 and a.allocate() == 4
+def test_allocation_order_is_ascending_then_lifo(kats):
+    c = kats["allocator_order"]
+    a = BlockAllocator(c["num_blocks"])
+    assert a.allocate_n(len(c["first"])) == c["first"]
+    a.free(c["free"])
+    assert [a.allocate() for _ in c["then"]] == c["then"]
 
 
 # --- sequence (reference tests/test_sequence.py) ----------------------------
 
-@pytest.mark.parametrize("n,expected", [(0, 0), (1, 1), (15, 1), (16, 1), (17, 2), (512, 32)])
-def test_blocks_for(n, expected):
-    assert blocks_for(n, 16) == expected
+def test_blocks_for(kats):
+    c = kats["blocks_for"]
+    for n, expected in c["cases"]:
+        assert blocks_for(n, c["block_size"]) == expected, n
 
 
 def test_growth_at_boundary():
@@ -113,10 +115,11 @@ def test_pool_shapes():
     assert not pool.kv.any()
 
 
-def test_pool_slot_mapping_kat():
+def test_pool_slot_mapping_kat(kats):
     pool = make_tiny_pool()
-    slots = pool.make_slot_mapping(start=14, n=4, block_table=[7, 3])
-    assert slots.dtype == torch.long and slots.tolist() == [126, 127, 48, 49]
+    for c in kats["slot_mapping"]:
+        slots = pool.make_slot_mapping(start=c["start"], n=c["n"], block_table=c["block_table"])
+        assert slots.dtype == torch.long and slots.tolist() == c["slots"]
 
 
 def test_pool_slot_mapping_asserts():
@@ -215,7 +218,7 @@ class FixedLogitModel(nn.Module):
         return logits
 
 
-def test_config1_block_tables_kat():
+def test_config1_block_tables_kat(kats):
     # 2 sequences, 16-token prompts, 80 greedy tokens, block_size 16,
     # 256 blocks: prefill allocates 1, 2; each 16-token boundary allocates
     # seq0 then seq1; final kv length 16 + 79 = 95 -> 6 blocks each
@@ -224,8 +227,9 @@ def test_config1_block_tables_kat():
     out = generate_batched(model, [list(range(16)), list(range(16, 32))], 80, None, a)
     assert [len(o) for o in out] == [80, 80]
     last = model.batches[-1]
-    assert last.block_tables == [[1, 3, 5, 7, 9, 11], [2, 4, 6, 8, 10, 12]]
-    assert last.positions == [94, 94] and last.seq_lens == [95, 95]
+    c = kats["config1_block_tables"]
+    assert last.block_tables == c["tables"]
+    assert last.positions == c["last_positions"] and last.seq_lens == c["last_seq_lens"]
     assert len(model.batches) == 80
     assert a.num_free == a.num_usable  # released in the finally block
     assert out[0][:3] == [1, 2, 3] and out[1][:3] == [2, 3, 4]

@@ -19,9 +19,11 @@ from oracle import torch_ref
 # slot mapping / append / gather
 # ---------------------------------------------------------------------------
 
-def test_slot_mapping_reference_kat():
+def test_slot_mapping_reference_kat(kats):
     # tests/test_kv_pool.py:25-30 of the reference
-    assert ref.make_slot_mapping(14, 4, [7, 3], 16).tolist() == [126, 127, 48, 49]
+    for c in kats["slot_mapping"]:
+        got = ref.make_slot_mapping(c["start"], c["n"], c["block_table"], c["block_size"])
+        assert got.tolist() == c["slots"]
 
 
 def test_slot_mapping_closed_form():
@@ -98,12 +100,14 @@ def test_gather_matches_torch_index_select():
 # metadata packing
 # ---------------------------------------------------------------------------
 
-def test_pack_metadata_kat():
-    table, lens, qloc, mql = ref.pack_metadata([[5, 2], [7]], [0, 3, 4], [17, 18, 19, 5], 4, 16)
-    assert table.tolist() == [[5, 2], [7, 0]]
-    assert lens.tolist() == [20, 6]
-    assert qloc.tolist() == [0, 3, 4]
-    assert mql == 3
+def test_pack_metadata_kat(kats):
+    for c in kats["pack_metadata"]:
+        table, lens, qloc, mql = ref.pack_metadata(c["block_tables"], c["query_start_loc"],
+                                                   c["positions"], c["T"], c["block_size"])
+        assert table.tolist() == c["table"]
+        assert lens.tolist() == c["seq_lens"]
+        assert qloc.tolist() == c["query_start_loc"]
+        assert mql == c["max_q_len"]
 
 
 def test_pack_metadata_errors():
@@ -196,6 +200,18 @@ def test_attention_vs_brute_force(causal):
     bo, bl = brute_force(p, causal=causal)
     np.testing.assert_allclose(out, bo, rtol=0, atol=1e-12)
     np.testing.assert_allclose(lse, bl, rtol=0, atol=1e-12)
+
+
+def test_attention_vs_golden_fixture(attention_golden):
+    # tests/golden/attention_small.npz: textbook outputs written by
+    # tests/golden/make_attention_golden.py, independent of the oracle
+    for name, c in attention_golden.items():
+        out, lse = ref.paged_attention(c["q"], c["k_pool"], c["v_pool"], c["block_table"],
+                                       c["seq_lens"], c["query_start_loc"])
+        np.testing.assert_allclose(out, c["out"], rtol=0, atol=1e-12, err_msg=name)
+        fin = np.isfinite(c["lse"])
+        assert np.array_equal(np.isfinite(lse), fin), name
+        np.testing.assert_allclose(lse[fin], c["lse"][fin], rtol=0, atol=1e-12, err_msg=name)
 
 
 @pytest.mark.parametrize("hq,hkv,d,bs", [(8, 1, 32, 16), (8, 8, 64, 16), (16, 4, 128, 16),
