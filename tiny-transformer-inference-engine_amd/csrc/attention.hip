@@ -300,8 +300,11 @@ int ceil_div_h(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 }  // namespace
 
 // Whether the persistent kernel takes this problem: one record per
-// (sequence, kv head) pair fits the workspace's record region.
-bool sk_fits(int64_t virt) { return virt >= 1 && virt <= kMaxCounters; }
+// (sequence, kv head) pair fits the workspace's record region, and every
+// table row has an entry (the kernel reads entry 0 of a row unconditionally).
+bool sk_fits(int64_t virt, int max_blk) {
+  return virt >= 1 && virt <= kMaxCounters && max_blk >= 1;
+}
 
 AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,
@@ -317,7 +320,7 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   // kernel, which gives every workgroup the same share of the actual work
   const bool persistent = part_tokens == PKV_PART_PERSISTENT ||
                           (part_tokens == 0 && kv_bound >= kSkAutoKv);
-  if (mfma && persistent && sk_fits(virt)) {
+  if (mfma && persistent && sk_fits(virt, max_blk)) {
     // persistent kernel: partials of at most two segments per workgroup
     p.kind = 2;
     p.rows = group;

@@ -55,6 +55,33 @@ __device__ __forceinline__ int sk_chunks(const AttnArgs& a, int v, int& kv_len) 
   return kv_len > 0 ? (kv_len + kChunk - 1) / kChunk : 1;
 }
 
+// chunks and clamped context of one sequence, as sk_chunks, from its
+// query_start_loc pair (q0, q1; 0, 1 without query_start_loc) and seq_len
+// (a malformed pair has been flagged by the scan's sk_chunks)
+struct SeqDesc {
+  int n, kv_len;
+};
+__device__ __forceinline__ SeqDesc seq_desc(const AttnArgs& a, int q0, int q1, int kl) {
+  SeqDesc d{0, 0};
+  if (a.qloc && (q1 - q0 <= 0 || q0 < 0 || q1 > a.n_tokens)) return d;
+  const int cap = a.max_blk << a.bs_shift;
+  kl = kl < cap ? kl : cap;
+  d.kv_len = kl > 0 ? kl : 0;
+  d.n = d.kv_len > 0 ? (d.kv_len + kChunk - 1) / kChunk : 1;
+  return d;
+}
+// The three loads are issued together whether or not query_start_loc is
+// given (without it, `alt` - any buffer of at least s + 2 ints - is read
+// and ignored), so they cost one round trip.
+__device__ __forceinline__ SeqDesc load_desc(const AttnArgs& a, int v, const int32_t* alt) {
+  const int s = v / a.hkv;
+  const int32_t* qsrc = a.qloc ? a.qloc : alt;
+  const int kl = ld_meta(a.seq_lens, s);
+  const int q0 = ld_meta(qsrc, s);
+  const int q1 = ld_meta(qsrc, s + 1);
+  return seq_desc(a, a.qloc ? q0 : 0, a.qloc ? q1 : 1, kl);
+}
+
 // first chunk of workgroup w's share, and the workgroup owning chunk x
 __device__ __forceinline__ int share_start(int w, int C, int W) {
   return (int)((int64_t)w * C / W);
@@ -182,27 +209,44 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   // uniform across the workgroup: scalar registers for the segment loop
   int v = __builtin_amdgcn_readfirstlane(s_v0);
   int g0 = __builtin_amdgcn_readfirstlane(s_g0);  // cost position where v's interval starts
+  SeqDesc dsc = load_desc(a, v, reinterpret_cast<const int32_t*>(k.recs));  // n > 0: the share's start lies in v's chunks
+  v8 qf[NT][D / 32];
+  {
+    const int s = v / a.hkv;
+    const int qtok = a.qloc ? ld_meta(a.qloc, s) : s;
+    load_q<T, D, NT>(qf, q, (int64_t)qtok * a.hq + (v - s * a.hkv) * G, grp, l16);
+  }
   bool first = true;
-  // sequence v's chunks sit at units [g0 + K, g0 + K + n); the share's
-  // chunks are those among [start, end)
-  while (g0 + K < end) {
-    int kv_len;
-    const int n = sk_chunks(a, v, kv_len);
-    if (n == 0) {
-      ++v;
-      continue;
-    }
+  bool prestaged = false;  // this segment's first table window (and new row) is in LDS
+  // Segment loop: sequence v's chunks sit at units [g0 + K, g0 + K + n) of
+  // the cost line; the share's chunks are those among [start, end). Once a
+  // segment has streamed, the next one's Q and first table window are loaded
+  // while this one's wavefront states are merged and written, so the next
+  // segment starts streaming without a dependent load.
+  for (;;) {
+    const int n = dsc.n;
+    const int kv_len = dsc.kv_len;
     const int c0 = max(0, start - (g0 + K));
     const int c1 = min(n, end - (g0 + K));
     const bool whole = c0 == 0 && c1 == n;
     const int s = v / a.hkv;
     const int kvh = v - s * a.hkv;
-    const int64_t qrow0 = (int64_t)(a.qloc ? a.qloc[s] : s) * a.hq + kvh * G;
+    const int qtok = a.qloc ? ld_meta(a.qloc, s) : s;
+    const int64_t qrow0 = (int64_t)qtok * a.hq + kvh * G;
     const int tok_lo = c0 * kChunk;
     const int tok_hi = min(c1 * kChunk, kv_len);
+    // the next sequence's metadata, in flight while this segment streams
+    const bool more = v + 1 < V;
+    int nq0 = 0, nq1 = 1, nkl = 0;
+    if (more) {
+      const int sn = (v + 1) / a.hkv;
+      if (a.qloc) {
+        nq0 = ld_meta(a.qloc, sn);
+        nq1 = ld_meta(a.qloc, sn + 1);
+      }
+      nkl = ld_meta(a.seq_lens, sn);
+    }
 
-    v8 qf[NT][D / 32];
-    load_q<T, D, NT>(qf, q, qrow0, grp, l16);
     // fused append: this share stages the new row when it covers its
     // position, and writes it into the pool when it holds the last chunk
     NewRow nr;
@@ -215,9 +259,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       const bool new_here = new_pos >= tok_lo && new_pos < tok_hi;
       new_write = c1 == n;
       if (new_here) nr.pos = new_pos;
-      new_pending = new_here || new_write;
+      new_pending = (new_here || new_write) && !prestaged;
     }
-    const int new_tok = (int)(qrow0 / a.hq);
     int last_blk_lo = 0, last_nblk = 0;
     pv.head_off = (int64_t)kvh * D * 2;
     const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
@@ -229,9 +272,11 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       cx.blk_lo = lo >> a.bs_shift;
       const int nblk = ((cx.seg_hi - 1) >> a.bs_shift) + 1 - cx.blk_lo;
       __syncthreads();  // previous window's table / slices / row buffer no longer read
-      if (APP && new_pending) {
+      if (prestaged && lo == tok_lo) {
+        // staged during the previous segment's merge
+      } else if (APP && new_pending) {
         // the new row's load is in flight with the table slice's
-        const u32x4 piece = load_new_row<D>(a, new_tok, kvh, tid);
+        const u32x4 piece = load_new_row<D>(a, qtok, kvh, tid);
         for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
         put_new_row<D>(new_lds, piece, tid);
         new_pending = false;
@@ -244,9 +289,45 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       last_nblk = nblk;
     }
     if (APP && new_write) {
-      if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, new_tok, kvh, tid), tid);
+      if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, qtok, kvh, tid), tid);
       // each thread stores the piece it put into the buffer itself
       store_new_row<D>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk, tid);
+    }
+
+    // ---- the next segment: its Q and first table window are loaded now
+    // (qf is free once this segment has streamed; the table and row buffer
+    // are written to LDS after the merge)
+    int v_n = v + 1;
+    const int g0_n = g0 + n + K;
+    SeqDesc d_n = seq_desc(a, nq0, nq1, nkl);
+    bool has_next = more && g0_n + K < end;
+    while (has_next && d_n.n == 0) {  // sequences without a query cost nothing
+      ++v_n;
+      has_next = v_n < V;
+      if (has_next) d_n = load_desc(a, v_n, reinterpret_cast<const int32_t*>(k.recs));
+    }
+    // Its first chunk is chunk 0 (g0_n + K lies past this segment's start).
+    // The loads are issued whether or not there is a next segment (then
+    // they re-read this one's rows, and are dropped): a load under a branch
+    // would cost the chunk loop its exact wait counts.
+    const int v_sel = has_next ? v_n : v;
+    const int s_n = v_sel / a.hkv;
+    const int kvh_n = v_sel - s_n * a.hkv;
+    const int qtok_n = a.qloc ? ld_meta(a.qloc, s_n) : s_n;
+    load_q<T, D, NT>(qf, q, (int64_t)qtok_n * a.hq + kvh_n * G, grp, l16);
+    const int c1_n = min(d_n.n, end - (g0_n + K));
+    const int tok_hi_n = min(c1_n * kChunk, d_n.kv_len);
+    const int n_nblk =
+        has_next && tok_hi_n > 0 ? ((min(win, tok_hi_n) - 1) >> a.bs_shift) + 1 : 0;
+    // max_blk >= 1 for this kernel: entry 0 of the row is always readable
+    const int tpref =
+        a.block_tables[(int64_t)s_n * a.max_blk + max(0, min(tid, n_nblk - 1))];
+    bool n_row = false;
+    u32x4 n_piece = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (APP) {
+      const int pos_n = a.new_pos[s_n];
+      n_row = has_next && ((pos_n >= 0 && pos_n < tok_hi_n) || c1_n == d_n.n);
+      n_piece = load_new_row<D>(a, qtok_n, kvh_n, tid);
     }
 
     // ---- merge the wavefronts' states through LDS ----
@@ -311,10 +392,16 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       const int w_last = share_owner(g0 + K + n - 1, C, W);
       k.recs[v] = make_int4(w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0, 0);
     }
-    __syncthreads();  // LDS merge area is reused by the next segment
-
-    g0 += n + K;
-    ++v;
+    __syncthreads();  // LDS merge area, table and row buffer are free
+    if (!has_next) break;
+    if (tid < n_nblk) tbl[tid] = tpref;  // published by the window loop's first barrier
+    if constexpr (APP) {
+      if (n_row) put_new_row<D>(new_lds, n_piece, tid);
+    }
+    prestaged = true;
+    v = v_n;
+    g0 = g0_n;
+    dsc = d_n;
     first = false;
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
@@ -327,10 +414,11 @@ constexpr int kMergeBlock = 256;
 template <typename T, int G, int D>
 __global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArgs k) {
   const int v = blockIdx.x;
-  int kv_len;
-  if (sk_chunks(a, v, kv_len) == 0) return;  // no query: nothing was recorded
-  const int4 r = k.recs[v];
-  const int w_first = r.x, w_last = r.y;
+  // the record and the sequence's metadata in one round trip (scalar loads)
+  const int32_t* rec = reinterpret_cast<const int32_t*>(k.recs) + 4 * (int64_t)v;
+  const int w_first = ld_meta(rec, 0), w_last = ld_meta(rec, 1), r_slot = ld_meta(rec, 2);
+  if (load_desc(a, v, reinterpret_cast<const int32_t*>(k.recs)).n == 0)
+    return;  // no query: nothing was recorded
   if (w_last <= w_first) return;  // finished in place
   const int idx = blockIdx.y * kMergeBlock + threadIdx.x;
   if (idx >= G * D / 4) return;
@@ -348,7 +436,7 @@ __global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArg
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
       const int ww = min(wb + j, w_last);
-      const int64_t sl = ww == w_first ? 2 * ww + r.z : 2 * ww;
+      const int64_t sl = ww == w_first ? 2 * ww + r_slot : 2 * ww;
       mm[j] = k.part_ml[(sl * G + head) * 2 + 0];
       ll[j] = k.part_ml[(sl * G + head) * 2 + 1];
       oo[j] = *reinterpret_cast<const floatx4*>(k.part_o + (sl * G + head) * D + d0);
@@ -369,7 +457,7 @@ __global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArg
   }
   const int s = v / a.hkv;
   const int kvh = v - s * a.hkv;
-  const int64_t qrow = (int64_t)(a.qloc ? a.qloc[s] : s) * a.hq + kvh * G + head;
+  const int64_t qrow = (int64_t)(a.qloc ? ld_meta(a.qloc, s) : s) * a.hq + kvh * G + head;
   const float inv = L > 0.f ? 1.f / L : 0.f;
   T* dst = static_cast<T*>(a.out) + qrow * D + d0;
   dst[0] = (T)(acc[0] * inv);

@@ -96,7 +96,7 @@ constexpr int kSkMaxWg = 512;  // workgroups of the persistent kernel, at most
 // A sequence's fixed cost in the persistent kernel (Q load, table slice,
 // wavefront merge, output or partial write) measured in 32-token chunks of
 // one workgroup's streaming time.
-constexpr int kSkSegCost = 3;
+constexpr int kSkSegCost = 7;
 // Context bound from which part_tokens = 0 selects the persistent kernel.
 constexpr int kSkAutoKv = 4096;
 
@@ -126,10 +126,21 @@ struct TileGeom {
   int q_begin, q_len, rows_here, kv_len, ctx, kv_limit, part_len, nparts;
 };
 
+// Loads through the scalar data cache: only for metadata no kernel of the
+// library writes (seq_lens, query_start_loc, block tables) or that an
+// earlier kernel wrote (the cache is invalidated at every launch), at an
+// index uniform across the wavefront. Unlike a vector load, waiting for one
+// does not wait for the wavefront's outstanding vector stores.
+typedef const __attribute__((address_space(4))) int32_t scalar_i32;
+__device__ __forceinline__ int ld_meta(const int32_t* p, int64_t i) {
+  return ((scalar_i32*)p)[i];
+}
+
 __device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
                                           int rows_per_tile, TileGeom& g) {
-  g.q_begin = a.qloc ? a.qloc[s] : s;
-  g.q_len = a.qloc ? a.qloc[s + 1] - g.q_begin : 1;
+  // s is uniform (it comes from the block index) in every caller
+  g.q_begin = a.qloc ? ld_meta(a.qloc, s) : s;
+  g.q_len = a.qloc ? ld_meta(a.qloc, s + 1) - g.q_begin : 1;
   if (g.q_len <= 0) return false;
   if (g.q_begin < 0 || g.q_begin + g.q_len > a.n_tokens) {
     // malformed query_start_loc: never index q / out outside [0, T)
@@ -140,7 +151,7 @@ __device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
   const int r0 = tile * rows_per_tile;
   if (r0 >= rows_total) return false;
   g.rows_here = min(rows_per_tile, rows_total - r0);
-  int kv_len = a.seq_lens[s];
+  int kv_len = ld_meta(a.seq_lens, s);
   const int cap = a.max_blk << a.bs_shift;
   kv_len = kv_len < cap ? kv_len : cap;
   g.kv_len = kv_len > 0 ? kv_len : 0;
