@@ -327,8 +327,7 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
     p.tiles_max = 1;
     p.part_tokens = 0;
     p.parts_max = 1;
-    p.ws_bytes = kWsCounterBytes +
-                 (size_t)kSkMaxWg * 2 * group * ((size_t)d + 2) * sizeof(float);
+    p.ws_bytes = sk_workspace_bytes(group, d);
     return p;
   }
   p.kind = mfma ? 1 : 0;
@@ -392,8 +391,8 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
     k.seg_cost = kSkSegCost;
     char* ws = reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes;
     k.recs = reinterpret_cast<int4*>(ws);
-    k.part_o = a.ws_o;
-    k.part_ml = k.part_o + (size_t)kSkMaxWg * 2 * a.group * a.d;
+    k.part_o = reinterpret_cast<_Float16*>(a.ws_o);
+    k.part_ml = reinterpret_cast<float*>(k.part_o + (size_t)kSkMaxWg * 2 * a.group * a.d);
     return launch_decode_sk(a, k, dtype, stream);
   }
   if (p.kind == 1) {

@@ -378,11 +378,15 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
         dst[3] = (T)(acc[3] * inv);
         if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
       } else {
-        *reinterpret_cast<floatx4*>(k.part_o + ((int64_t)slot * G + head) * D + d0) = acc;
-        if (d0 == 0) {
-          k.part_ml[((int64_t)slot * G + head) * 2 + 0] = M;
-          k.part_ml[((int64_t)slot * G + head) * 2 + 1] = L;
-        }
+        // normalised by its own sum (a weighted mean of value rows, so its
+        // range is theirs) and rounded to fp16: half the partial traffic
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        *reinterpret_cast<half4*>(k.part_o + ((int64_t)slot * G + head) * D + d0) =
+            half4{(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
+                  (_Float16)(acc[3] * inv)};
+        if (d0 == 0)
+          *reinterpret_cast<float2*>(k.part_ml + ((int64_t)slot * G + head) * 2) =
+              make_float2(M, L);
       }
     }
 
@@ -428,8 +432,8 @@ __global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArg
   float M = -INFINITY, L = 0.f;
   floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
   for (int wb = w_first; wb <= w_last; wb += kMB) {
-    float mm[kMB], ll[kMB];
-    floatx4 oo[kMB];
+    float2 ml[kMB];
+    half4 oo[kMB];
     // branch-free: contributors past w_last re-read w_last's partial and are
     // dropped afterwards, so no load sits under a branch (a branch join
     // would make the compiler wait for every load issued before it)
@@ -437,21 +441,21 @@ __global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArg
     for (int j = 0; j < kMB; ++j) {
       const int ww = min(wb + j, w_last);
       const int64_t sl = ww == w_first ? 2 * ww + r_slot : 2 * ww;
-      mm[j] = k.part_ml[(sl * G + head) * 2 + 0];
-      ll[j] = k.part_ml[(sl * G + head) * 2 + 1];
-      oo[j] = *reinterpret_cast<const floatx4*>(k.part_o + (sl * G + head) * D + d0);
+      ml[j] = *reinterpret_cast<const float2*>(k.part_ml + (sl * G + head) * 2);
+      oo[j] = *reinterpret_cast<const half4*>(k.part_o + (sl * G + head) * D + d0);
     }
 #pragma unroll
     for (int j = 0; j < kMB; ++j)
-      if (wb + j > w_last) mm[j] = -INFINITY;
+      if (wb + j > w_last) ml[j].x = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
-      if (mm[j] == -INFINITY) continue;
-      const float Mn = fmaxf(M, mm[j]);
+      if (ml[j].x == -INFINITY) continue;
+      const float Mn = fmaxf(M, ml[j].x);
       const float sa = exp2f(M - Mn);
-      const float sb = exp2f(mm[j] - Mn);
-      L = L * sa + ll[j] * sb;
-      acc = acc * sa + oo[j] * sb;
+      const float wl = ml[j].y * exp2f(ml[j].x - Mn);  // this partial's weight
+      L = L * sa + wl;
+      acc = acc * sa + floatx4{(float)oo[j][0], (float)oo[j][1], (float)oo[j][2],
+                               (float)oo[j][3]} * wl;
       M = Mn;
     }
   }

@@ -28,6 +28,7 @@ namespace pkv {
 namespace mfma {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>

@@ -104,9 +104,15 @@ struct SkArgs {
   int n_wg;         // workgroups launched
   int seg_cost;     // overhead of one sequence in chunk units (share balance)
   int4* recs;       // [n_seq * hkv] (first, last contributor, first's slot)
-  float* part_o;    // [n_wg][2][G][D] partial outputs
+  _Float16* part_o; // [n_wg][2][G][D] partial outputs, normalised (O / sum)
   float* part_ml;   // [n_wg][2][G][2] partial (max, sum)
 };
+
+// Workspace of the persistent kernel: the record header, then the fp16
+// partial outputs and the fp32 (max, sum) pairs of two slots per workgroup.
+inline size_t sk_workspace_bytes(int group, int d) {
+  return kWsCounterBytes + (size_t)kSkMaxWg * 2 * group * ((size_t)d * 2 + 2 * 4);
+}
 
 struct AttnPlan {
   int kind;        // 0 = generic rows kernel, 1 = MFMA partition kernel,
