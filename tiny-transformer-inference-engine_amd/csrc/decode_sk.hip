@@ -94,23 +94,31 @@ __device__ __forceinline__ int share_owner(int x, int C, int W) {
 // seg_cost overhead units plus its chunks.
 __device__ __forceinline__ int sk_cost(int n, int seg_cost) { return n > 0 ? n + seg_cost : 0; }
 
-// block-wide exclusive scan of one int per thread; returns the total
+// block-wide exclusive scan of one int per thread; returns the total.
+// Each wavefront scans its 64 values with lane shuffles, then the
+// wavefront totals are combined through LDS (two barriers in all).
 __device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
-  const int t = threadIdx.x;
-  sh[t] = x;
-  __syncthreads();
-  for (int off = 1; off < kBlock; off <<= 1) {
-    const int y = t >= off ? sh[t - off] : 0;
-    __syncthreads();
-    sh[t] += y;
-    __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  int incl = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
   }
-  const int incl = sh[t];
-  // the same for every thread: keep it scalar
-  const int total = __builtin_amdgcn_readfirstlane(sh[kBlock - 1]);
+  if (lane == 63) sh[w] = incl;
   __syncthreads();
-  excl = incl - x;
-  return total;
+  int before = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    const int t = sh[i];
+    before += i < w ? t : 0;
+    total += t;
+  }
+  __syncthreads();  // sh is reused by the next scan
+  excl = before + incl - x;
+  // the same for every thread: keep it scalar
+  return __builtin_amdgcn_readfirstlane(total);
 }
 
 template <typename T, int D, int NT, int PF, bool OFF64, bool APP>
