@@ -208,40 +208,47 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a,
   const int tile = blockIdx.y;
   const int s = blockIdx.x / a.hkv;
   const int kvh = blockIdx.x - s * a.hkv;
-  TileGeom g;
-  if (!tile_geom(a, s, tile, rows_per_tile, g)) return;
-  if (g.nparts == 1) return;
   const int D = a.d;
   const int quads = D / 4;
   const int item = blockIdx.z * kThreads + threadIdx.x;
   const int r = item / quads;
-  if (r >= g.rows_here) return;
   const int d0 = (item - r * quads) * 4;
+  const int64_t unit0 = ((int64_t)blockIdx.x * a.tiles_max + tile) * a.parts_max;
+  // One pass with a running max; the loads of kMB partitions are issued
+  // before any is consumed and never sit under a branch (a branch join
+  // would make the compiler wait for every load issued before it), so the
+  // merge costs ceil(nparts / kMB) memory latencies. The first batch is
+  // requested before the sequence's metadata: rows and partitions past the
+  // ones that exist are read from the workspace (in bounds) and dropped.
+  constexpr int kMB = 8;
+  const int rr = min(r, rows_per_tile - 1);
+  float mm[kMB], ll[kMB];
+  float4 oo[kMB];
+  auto load_batch = [&](int p0, int last) {
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      const int64_t row = (unit0 + min(p0 + j, last)) * rows_per_tile + rr;
+      mm[j] = a.ws_ml[row * 2];
+      ll[j] = a.ws_ml[row * 2 + 1];
+      oo[j] = *reinterpret_cast<const float4*>(a.ws_o + row * D + d0);
+    }
+  };
+  load_batch(0, a.parts_max - 1);
+  TileGeom g;
+  if (!tile_geom(a, s, tile, rows_per_tile, g)) return;
+  if (g.nparts == 1) return;
+  if (r >= g.rows_here) return;
   const int G = a.group;
   const int rg = tile * rows_per_tile + r;
   const int i = rg / G;
   const int h = rg - i * G;
   const int64_t qrow = (int64_t)(g.q_begin + i) * a.hq + kvh * G + h;
-  const int64_t unit0 = ((int64_t)blockIdx.x * a.tiles_max + tile) * a.parts_max;
   T* __restrict__ out = static_cast<T*>(a.out) + qrow * D + d0;
-  // one pass with a running max; the loads of kMB partitions are issued
-  // before any is consumed and never sit under a branch (a branch join
-  // would make the compiler wait for every load issued before it), so the
-  // merge costs ceil(nparts / kMB) memory latencies
-  constexpr int kMB = 8;
   float M = -INFINITY;
   float L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int p0 = 0; p0 < g.nparts; p0 += kMB) {
-    float mm[kMB], ll[kMB];
-    float4 oo[kMB];
-#pragma unroll
-    for (int j = 0; j < kMB; ++j) {
-      const int64_t row = (unit0 + min(p0 + j, g.nparts - 1)) * rows_per_tile + r;
-      mm[j] = a.ws_ml[row * 2];
-      ll[j] = a.ws_ml[row * 2 + 1];
-      oo[j] = *reinterpret_cast<const float4*>(a.ws_o + row * D + d0);
-    }
+    if (p0 > 0) load_batch(p0, g.nparts - 1);
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
       if (p0 + j >= g.nparts || mm[j] == -INFINITY) continue;
@@ -311,7 +318,9 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int part_tokens, int dtype) {
   AttnPlan p{};
   const int group = hq / hkv;
-  const bool mfma = decode_mfma_supported(dtype, max_q_len, group, d);
+  // the MFMA kernels read table entry 0 of a row unconditionally: with no
+  // table (every context empty) the generic kernel writes the empty rows
+  const bool mfma = decode_mfma_supported(dtype, max_q_len, group, d) && max_blk >= 1;
   const int64_t virt = (int64_t)n_seq * hkv;
   const int64_t cap_tokens = (int64_t)max_blk * block_size;
   const int64_t kv_bound = max_kv_len > 0 && max_kv_len < cap_tokens ? max_kv_len : cap_tokens;

@@ -24,6 +24,7 @@ using namespace mfma;
 
 constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
+static_assert(kBlock >= kTblCap, "one thread per table entry of a window");
 
 // PF = chunks each wavefront keeps in flight in registers; OCC = wavefronts
 // per SIMD the register budget is sized for; APP = the fused append of
@@ -50,17 +51,26 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   const int part = blockIdx.y;
   const int s = blockIdx.x / a.hkv;
   const int kvh = blockIdx.x - s * a.hkv;
+  const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
+  const T* __restrict__ q = static_cast<const T*>(a.q);
+  // Requested before the sequence's metadata arrives: the partition's first
+  // table window at the planned partition length (one entry per thread,
+  // entries past the table's end clamped and unused) and, without
+  // query_start_loc, the Q rows (query token s).
+  const int spec_blk0 = (part * a.part_tokens) >> a.bs_shift;
+  const int tspec = table[max(0, min(spec_blk0 + (int)threadIdx.x, a.max_blk - 1))];
+  v8 qf[NT][D / 32];
+  if (!a.qloc) load_q<T, D, NT>(qf, q, (int64_t)s * a.hq + kvh * G, grp, l16);
   TileGeom g;
   if (!tile_geom(a, s, 0, G, g)) return;
   if (part >= g.nparts) return;
   const int kv_lo = part * g.part_len;
   const int kv_hi = min(kv_lo + g.part_len, g.kv_limit);
-  const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
-
-  const T* __restrict__ q = static_cast<const T*>(a.q);
   const int64_t qrow0 = (int64_t)g.q_begin * a.hq + kvh * G;
-  v8 qf[NT][D / 32];
-  load_q<T, D, NT>(qf, q, qrow0, grp, l16);
+  if (a.qloc) load_q<T, D, NT>(qf, q, qrow0, grp, l16);
+  // the speculative window is this partition's first one unless the
+  // sequence outgrew the planned bound (longer partitions)
+  const bool spec_ok = g.part_len == a.part_tokens;
 
   PoolView pv;
   pv.kbase = static_cast<const char*>(a.k_pool);
@@ -108,12 +118,19 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     cx.blk_lo = lo >> a.bs_shift;
     const int nblk = ((cx.seg_hi - 1) >> a.bs_shift) + 1 - cx.blk_lo;
     __syncthreads();  // previous window's table no longer read
+    const bool spec = spec_ok && lo == kv_lo;
     if (APP && new_pending) {
       // the new row's load is in flight with the table slice's
       const u32x4 piece = load_new_row<D>(a, g.q_begin, kvh, threadIdx.x);
-      for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+      if (spec) {
+        if ((int)threadIdx.x < nblk) tbl[threadIdx.x] = tspec;
+      } else {
+        for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+      }
       put_new_row<D>(new_lds, piece, threadIdx.x);
       new_pending = false;
+    } else if (spec) {
+      if ((int)threadIdx.x < nblk) tbl[threadIdx.x] = tspec;
     } else {
       for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
     }
