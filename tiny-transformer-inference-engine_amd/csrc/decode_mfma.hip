@@ -150,8 +150,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   // ---- merge the 4 wavefronts' partial states through LDS ----
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    st.l[nt] += __shfl_xor(st.l[nt], 16);
-    st.l[nt] += __shfl_xor(st.l[nt], 32);
+    st.l[nt] = head_lanes_sum(st.l[nt]);
   }
   __syncthreads();  // every wavefront is done with its K/V slice
   float* ob = reinterpret_cast<float*>(lds);

@@ -341,8 +341,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     // ---- merge the wavefronts' states through LDS ----
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      st.l[nt] += __shfl_xor(st.l[nt], 16);
-      st.l[nt] += __shfl_xor(st.l[nt], 32);
+      st.l[nt] = head_lanes_sum(st.l[nt]);
     }
     __syncthreads();
 #pragma unroll

@@ -141,6 +141,29 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NPL>& r, const PoolView& pv
   r.valid = vmask;
 }
 
+// Max / sum over the four lanes of a head (lanes l, l + 16, l + 32, l + 48)
+// by the cross-row swaps of gfx950 (v_permlane16_swap, v_permlane32_swap:
+// VALU data movement, no LDS round trip). After a swap of x with itself the
+// two results hold rows (0, 0, 2, 2) and (1, 1, 3, 3) (resp. halves
+// (lo, lo) and (hi, hi)), so every lane combines the same operands in the
+// same order and all four end with identical bits.
+__device__ __forceinline__ float head_lanes_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float head_lanes_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Online-softmax state of one wavefront: lane l holds head 16*nt + l%16,
 // output dims 16*dt + 4*(l/16) + 0..3.
 template <int NT, int DT>
@@ -267,8 +290,7 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
       float mx = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sv[nt][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = head_lanes_max(mx);
       const float m_new = fmaxf(st.m[nt], mx);
       const float alpha = m_new == -INFINITY ? 1.f : exp2f(st.m[nt] - m_new);
       st.l[nt] *= alpha;
