@@ -1,0 +1,111 @@
+"""Batches that mix decode sequences (one query token) with chunked-prefill
+sequences (many), as in BASELINE config 5's step (256 decodes + a 512-token
+chunked-prefill append for 4 new sequences). One library call splits such a
+batch: the decode sequences run on an MFMA decode kernel, the prefill
+sequences on the prefill kernel.
+
+  - outputs and lse against the fp64 oracle (bf16 / fp16: 2e-2 absolute),
+    with the decode part on the split-K partition kernel, the persistent
+    kernel, and the automatic choice;
+  - fused append (pkv_paged_attention_append) of such a batch against
+    KVPool.write_from_table + attention: pools and outputs bit-identical;
+  - sequences without a query this step inside the mixed batch.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_ref as ref
+from serving import _native, workloads
+from serving.fake_paged_attn import paged_attention_append_meta, paged_attention_meta
+from serving.kv_pool import KVPool
+from serving.paged_meta import pack_batch_meta
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def mixed_batch(n_dec, chunks, hq, d, dtype, bs, seed, empty=()):
+    """n_dec decode sequences (lognormal contexts, one new token each) then
+    len(chunks) prefill sequences; chunks[i] = (prior context, chunk tokens).
+    Sequences listed in `empty` get no query this step."""
+    dec_lens = workloads.lengths_lognormal(n_dec, 600, 3000, seed)
+    q_lens, starts = [], []
+    for i, L in enumerate(dec_lens):
+        q_lens.append(0 if i in empty else 1)
+        starts.append(int(L))
+    for prior, n in chunks:
+        q_lens.append(n)
+        starts.append(prior)
+    ends = [s + q for s, q in zip(starts, q_lens)]
+    tables = workloads.permuted_tables([max(e, s + 1) for s, e in zip(starts, ends)], bs,
+                                       1 << 15, seed)
+    pool = KVPool(1, bs, 1 << 15, 1, d, dtype, torch.device(DEV))
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    pool.kv.normal_(generator=g)
+    T = sum(q_lens)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int64).tolist()
+    positions = [p for s, q in zip(starts, q_lens) for p in range(s, s + q)]
+    meta = pack_batch_meta(tables, qsl, positions, T, torch.device(DEV), bs)
+    q = torch.randn(T, hq, d, generator=g, device=DEV).to(dtype)
+    k = torch.randn(T, 1, d, generator=g, device=DEV).to(dtype)
+    v = torch.randn(T, 1, d, generator=g, device=DEV).to(dtype)
+    return pool, meta, q, k, v
+
+
+def oracle(pool, meta, q):
+    return ref.paged_attention(np64(q), np64(pool.kv[0, 0]), np64(pool.kv[0, 1]),
+                               meta.block_tables.cpu().numpy(), meta.seq_lens.cpu().numpy(),
+                               meta.query_start_loc.cpu().numpy())
+
+
+@pytest.mark.parametrize("part_tokens", [0, 512, _native.PART_PERSISTENT],
+                         ids=["auto", "partition", "persistent"])
+@pytest.mark.parametrize("hq,d,dtype", [(32, 128, torch.bfloat16), (16, 64, torch.float16)])
+def test_mixed_batch_vs_oracle(part_tokens, hq, d, dtype):
+    print(f"[mixed] hq={hq} d={d} {dtype} part_tokens={part_tokens}", flush=True)
+    # 4 new sequences' 128-token chunks (no prior context) and one later
+    # chunk of a longer prompt
+    pool, meta, q, k, v = mixed_batch(48, [(0, 128), (0, 128), (0, 128), (0, 128), (700, 96)],
+                                      hq, d, dtype, 16, seed=31, empty=(5,))
+    pool.write_from_table(0, k, v, meta)
+    lse = torch.empty(q.shape[0], hq, device=DEV)
+    out = torch.empty_like(q)
+    from serving.fake_paged_attn import _launch
+    _launch(q, pool.kv[0, 0], pool.kv[0, 1], meta.block_tables, meta.seq_lens,
+            meta.query_start_loc, meta.num_seqs, meta.max_q_len, meta.max_kv_len, 0.0, True,
+            out, lse, part_tokens)
+    torch.cuda.synchronize()
+    eo, el = oracle(pool, meta, q)
+    got = np64(out)
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - eo).max()
+    assert err <= 2e-2, f"max err {err:.3e}"
+    fin = np.isfinite(el)
+    np.testing.assert_allclose(lse.cpu().numpy()[fin], el[fin], rtol=0, atol=2e-2)
+
+
+@pytest.mark.parametrize("bound", [0, 8192])
+def test_mixed_batch_fused_append_equals_two_calls(bound):
+    print(f"[mixed fused] bound={bound}", flush=True)
+    pool_a, meta, q, k, v = mixed_batch(64, [(0, 128), (0, 128), (300, 128), (0, 128)], 32, 128,
+                                        torch.bfloat16, 16, seed=32)
+    if bound:
+        meta.max_kv_len = bound  # the persistent decode kernel
+    pool_b = KVPool(1, 16, pool_a.num_blocks, 1, 128, torch.bfloat16, torch.device(DEV))
+    pool_b.kv.copy_(pool_a.kv)
+    lse_a = torch.empty(q.shape[0], 32, device=DEV)
+    lse_b = torch.empty(q.shape[0], 32, device=DEV)
+    pool_a.write_from_table(0, k, v, meta)
+    out_a = paged_attention_meta(q, pool_a.kv[0, 0], pool_a.kv[0, 1], meta, lse=lse_a)
+    out_b = paged_attention_append_meta(q, k, v, pool_b, 0, meta, lse=lse_b)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a.kv, pool_b.kv), "pools differ"
+    assert torch.equal(out_a, out_b), "outputs differ"
+    assert torch.equal(lse_a, lse_b), "lse differs"
+    eo, _ = oracle(pool_a, meta, q)
+    assert np.abs(np64(out_b) - eo).max() <= 2e-2

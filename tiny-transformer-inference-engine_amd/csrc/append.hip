@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void append_table_kernel(
     const char* __restrict__ v_new, const int32_t* __restrict__ tables,
     int max_blk, const int32_t* __restrict__ qloc,
     const int32_t* __restrict__ start_pos, int n_seq, int64_t n_tok,
-    int64_t row_bytes, int* status) {
+    int64_t row_bytes, int min_qlen, int* status) {
   using V = typename VecT<VEC>::type;
   const int64_t ppr = row_bytes / VEC;
   const int64_t total = n_tok * ppr;
@@ -96,6 +96,9 @@ __global__ __launch_bounds__(kThreads) void append_table_kernel(
     const int64_t tok = i / ppr;
     const int64_t pc = i - tok * ppr;
     const int s = seq_of_token(qloc, n_seq, tok);
+    // rows of sequences with fewer than min_qlen tokens are another
+    // launch's (the fused decode append of a mixed batch)
+    if (min_qlen > 1 && qloc[s + 1] - qloc[s] < min_qlen) continue;
     const int64_t pos = (int64_t)start_pos[s] + (tok - qloc[s]);
     const int64_t page = pos >> bs_shift;
     const bool flag = status && pc == 0 && blockIdx.y == 0;
@@ -192,8 +195,8 @@ int launch_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
                              const void* v_new, const int32_t* block_tables,
                              int max_blk, const int32_t* qloc,
                              const int32_t* start_pos, int n_seq,
-                             int64_t n_tok, int64_t row_bytes, int* status,
-                             hipStream_t stream) {
+                             int64_t n_tok, int64_t row_bytes, int min_qlen,
+                             int* status, hipStream_t stream) {
   if (n_tok == 0 || n_seq == 0) return PKV_OK;
   const int vec = pick_vec(row_bytes, {k_pool, v_pool, k_new, v_new});
   const dim3 grid = copy_grid(n_tok * (row_bytes / vec));
@@ -202,7 +205,7 @@ int launch_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
                      stream, (char*)k_pool, (char*)v_pool, num_blocks,       \
                      bs_shift, (const char*)k_new, (const char*)v_new,       \
                      block_tables, max_blk, qloc, start_pos, n_seq, n_tok,   \
-                     row_bytes, status)
+                     row_bytes, min_qlen, status)
   switch (vec) {
     case 16: PKV_APPEND_T(16); break;
     case 8: PKV_APPEND_T(8); break;

@@ -374,6 +374,26 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   return p;
 }
 
+AttnSplit plan_split(int n_seq, int max_q_len, int hq, int hkv, int d, int max_blk,
+                     int block_size, int max_kv_len, int part_tokens, int dtype,
+                     bool has_qloc) {
+  AttnSplit sp{};
+  sp.mixed = has_qloc && max_q_len > 1 && n_seq >= 2 && max_blk >= 1 &&
+             decode_mfma_supported(dtype, 1, hq / hkv, d);
+  if (!sp.mixed) {
+    sp.dec = plan_attention(n_seq, max_q_len, hq, hkv, d, max_blk, block_size, max_kv_len,
+                            part_tokens, dtype);
+    sp.ws_bytes = sp.dec.ws_bytes;
+    return sp;
+  }
+  sp.dec = plan_attention(n_seq, 1, hq, hkv, d, max_blk, block_size, max_kv_len, part_tokens,
+                          dtype);
+  sp.pre = plan_attention(n_seq, max_q_len, hq, hkv, d, max_blk, block_size, max_kv_len,
+                          part_tokens, dtype);
+  sp.ws_bytes = sp.dec.ws_bytes > sp.pre.ws_bytes ? sp.dec.ws_bytes : sp.pre.ws_bytes;
+  return sp;
+}
+
 int device_cu_count() {
   static int cache[64] = {0};
   int dev = 0;

@@ -91,7 +91,7 @@ int pkv_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
   return launch_append_from_table(
       k_pool, v_pool, num_blocks, bs_shift, k_new, v_new, block_tables,
       max_blk, query_start_loc, start_pos, n_seq, n_tok,
-      row_elems * elem_bytes(dtype), status, (hipStream_t)stream);
+      row_elems * elem_bytes(dtype), 0, status, (hipStream_t)stream);
 }
 
 int pkv_gather(void* k_out, void* v_out, const void* k_pool,
@@ -124,8 +124,9 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
                                      int dtype) {
   if (n_seq <= 0 || max_q_len <= 0 || hkv <= 0 || hq <= 0 || hq % hkv != 0)
     return 0;
-  return plan_attention(n_seq, max_q_len, hq, hkv, d, max_blk, block_size,
-                        max_kv_len, part_tokens, dtype)
+  // query_start_loc is required whenever max_q_len > 1
+  return plan_split(n_seq, max_q_len, hq, hkv, d, max_blk, block_size, max_kv_len,
+                    part_tokens, dtype, max_q_len > 1)
       .ws_bytes;
 }
 
@@ -163,60 +164,86 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     return fail(PKV_ERR_INVALID, "null pointer argument");
   if (!query_start_loc && max_q_len != 1)
     return fail(PKV_ERR_INVALID, "query_start_loc may be NULL only when max_q_len == 1");
-  const AttnPlan plan = plan_attention(n_seq, max_q_len, hq, hkv, d, max_blk,
-                                       block_size, max_kv_len, part_tokens,
-                                       dtype);
-  if (plan.ws_bytes > 0 && (!workspace || workspace_bytes < plan.ws_bytes))
+  const AttnSplit sp = plan_split(n_seq, max_q_len, hq, hkv, d, max_blk, block_size,
+                                  max_kv_len, part_tokens, dtype, query_start_loc != nullptr);
+  if (sp.ws_bytes > 0 && (!workspace || workspace_bytes < sp.ws_bytes))
     return fail(PKV_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given",
-                plan.ws_bytes, workspace ? workspace_bytes : (size_t)0);
+                sp.ws_bytes, workspace ? workspace_bytes : (size_t)0);
   const float sc = scale > 0.f ? scale : 1.f / sqrtf((float)d);
-  AttnArgs a{};
-  a.out = out;
-  a.lse = lse;
-  a.q = q;
-  a.k_pool = k_pool;
-  a.v_pool = v_pool;
-  a.block_tables = block_tables;
-  a.seq_lens = seq_lens;
-  a.qloc = query_start_loc;
-  a.num_blocks = num_blocks;
-  a.bs_shift = bs_shift;
-  a.max_blk = max_blk;
-  a.n_seq = n_seq;
-  a.n_tokens = n_tokens;
-  a.hq = hq;
-  a.hkv = hkv;
-  a.group = hq / hkv;
-  a.d = d;
-  a.scale_log2 = sc * 1.4426950408889634f;
-  a.causal = causal ? 1 : 0;
-  a.part_tokens = plan.part_tokens;
-  a.parts_max = plan.parts_max;
-  a.tiles_max = plan.tiles_max;
-  // partials live after the counter region (see kWsCounterBytes)
-  float* ws = plan.ws_bytes
-                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kWsCounterBytes)
-                  : nullptr;
-  const size_t units = (size_t)n_seq * hkv * plan.tiles_max * plan.parts_max;
-  a.ws_o = ws;
-  a.ws_ml = ws ? ws + units * plan.rows * (size_t)d : nullptr;
-  a.status = status;
-  if (k_new) {
-    if (plan.kind == 0) {
-      // no fused form for the generic kernel: append, then attend
-      const int rc = launch_append_from_table(
-          const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
-          v_new, block_tables, max_blk, query_start_loc, start_pos,
-          n_seq, n_tokens, (int64_t)hkv * d * elem_bytes(dtype), status,
-          (hipStream_t)stream);
-      if (rc != PKV_OK) return rc;
-    } else {
-      a.k_new = k_new;
-      a.v_new = v_new;
-      a.new_pos = start_pos;
+  AttnArgs base{};
+  base.out = out;
+  base.lse = lse;
+  base.q = q;
+  base.k_pool = k_pool;
+  base.v_pool = v_pool;
+  base.block_tables = block_tables;
+  base.seq_lens = seq_lens;
+  base.qloc = query_start_loc;
+  base.num_blocks = num_blocks;
+  base.bs_shift = bs_shift;
+  base.max_blk = max_blk;
+  base.n_seq = n_seq;
+  base.n_tokens = n_tokens;
+  base.hq = hq;
+  base.hkv = hkv;
+  base.group = hq / hkv;
+  base.d = d;
+  base.scale_log2 = sc * 1.4426950408889634f;
+  base.causal = causal ? 1 : 0;
+  base.status = status;
+  // one launch's view: its plan's geometry and workspace layout (partials
+  // live after the record region, see kWsCounterBytes)
+  auto args_for = [&](const AttnPlan& plan, int qfilter) {
+    AttnArgs a = base;
+    a.qfilter = qfilter;
+    a.part_tokens = plan.part_tokens;
+    a.parts_max = plan.parts_max;
+    a.tiles_max = plan.tiles_max;
+    float* ws = plan.ws_bytes ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                         kWsCounterBytes)
+                              : nullptr;
+    const size_t units = (size_t)n_seq * hkv * plan.tiles_max * plan.parts_max;
+    a.ws_o = ws;
+    a.ws_ml = ws ? ws + units * plan.rows * (size_t)d : nullptr;
+    return a;
+  };
+  const int64_t row_bytes = (int64_t)hkv * d * elem_bytes(dtype);
+  if (!sp.mixed) {
+    AttnArgs a = args_for(sp.dec, 0);
+    if (k_new) {
+      if (sp.dec.kind == 0) {
+        // no fused form for the generic kernel: append, then attend
+        const int rc = launch_append_from_table(
+            const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
+            v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens,
+            row_bytes, 0, status, (hipStream_t)stream);
+        if (rc != PKV_OK) return rc;
+      } else {
+        a.k_new = k_new;
+        a.v_new = v_new;
+        a.new_pos = start_pos;
+      }
     }
+    return launch_attention(a, sp.dec, dtype, (hipStream_t)stream);
   }
-  return launch_attention(a, plan, dtype, (hipStream_t)stream);
+  // mixed batch: the decode sequences on an MFMA decode kernel (with their
+  // append fused), then the prefill sequences, whose rows are appended
+  // first because the prefill kernel reads them from the pool
+  AttnArgs ad = args_for(sp.dec, 1);
+  const AttnArgs ap = args_for(sp.pre, 2);
+  if (k_new) {
+    const int rc = launch_append_from_table(
+        const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
+        v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens, row_bytes,
+        2, status, (hipStream_t)stream);
+    if (rc != PKV_OK) return rc;
+    ad.k_new = k_new;
+    ad.v_new = v_new;
+    ad.new_pos = start_pos;
+  }
+  int rc = launch_attention(ad, sp.dec, dtype, (hipStream_t)stream);
+  if (rc != PKV_OK) return rc;
+  return launch_attention(ap, sp.pre, dtype, (hipStream_t)stream);
 }
 
 }  // namespace

@@ -42,7 +42,7 @@ __device__ __forceinline__ int sk_chunks(const AttnArgs& a, int v, int& kv_len) 
   if (a.qloc) {
     const int q0 = a.qloc[s];
     const int ql = a.qloc[s + 1] - q0;
-    if (ql <= 0) return 0;
+    if (ql <= 0 || (a.qfilter == 1 && ql != 1)) return 0;
     if (q0 < 0 || q0 + ql > a.n_tokens) {
       if (a.status) atomicOr(a.status, PKV_STATUS_BAD_QLOC);
       return 0;
@@ -63,7 +63,9 @@ struct SeqDesc {
 };
 __device__ __forceinline__ SeqDesc seq_desc(const AttnArgs& a, int q0, int q1, int kl) {
   SeqDesc d{0, 0};
-  if (a.qloc && (q1 - q0 <= 0 || q0 < 0 || q1 > a.n_tokens)) return d;
+  if (a.qloc && (q1 - q0 <= 0 || q0 < 0 || q1 > a.n_tokens ||
+                 (a.qfilter == 1 && q1 - q0 != 1)))
+    return d;
   const int cap = a.max_blk << a.bs_shift;
   kl = kl < cap ? kl : cap;
   d.kv_len = kl > 0 ? kl : 0;

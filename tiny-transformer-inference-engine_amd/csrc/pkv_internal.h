@@ -36,8 +36,8 @@ int launch_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
                              const void* v_new, const int32_t* block_tables,
                              int max_blk, const int32_t* qloc,
                              const int32_t* start_pos, int n_seq,
-                             int64_t n_tok, int64_t row_bytes, int* status,
-                             hipStream_t stream);
+                             int64_t n_tok, int64_t row_bytes, int min_qlen,
+                             int* status, hipStream_t stream);
 
 int launch_gather(void* k_out, void* v_out, const void* k_pool,
                   const void* v_pool, int64_t num_blocks, int bs_shift,
@@ -67,6 +67,10 @@ struct AttnArgs {
   int d;
   float scale_log2;  // softmax scale * log2(e)
   int causal;
+  // which sequences this launch handles (a mixed batch is split between the
+  // decode and the prefill kernels): 0 every one, 1 only those with one
+  // query token, 2 only those with more
+  int qfilter;
   int part_tokens;   // split-K partition length (multiple of 32)
   int parts_max;     // partitions per (sequence, kv head, row tile) in grid
   int tiles_max;     // row tiles per (sequence, kv head) in grid
@@ -148,6 +152,7 @@ __device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
   g.q_begin = a.qloc ? ld_meta(a.qloc, s) : s;
   g.q_len = a.qloc ? ld_meta(a.qloc, s + 1) - g.q_begin : 1;
   if (g.q_len <= 0) return false;
+  if ((a.qfilter == 1 && g.q_len != 1) || (a.qfilter == 2 && g.q_len == 1)) return false;
   if (g.q_begin < 0 || g.q_begin + g.q_len > a.n_tokens) {
     // malformed query_start_loc: never index q / out outside [0, T)
     if (a.status && tile == 0) atomicOr(a.status, PKV_STATUS_BAD_QLOC);
@@ -181,6 +186,21 @@ __device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
 AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,
                         int part_tokens, int dtype);
+
+// A batch that may mix single-token (decode) and multi-token (prefill)
+// queries is split when the decode sequences can take an MFMA decode
+// kernel: `dec` handles the sequences with one query token, `pre` the
+// others, launched one after the other on the stream and sharing the
+// workspace (ws_bytes is the larger need). Otherwise `dec` is the one plan.
+struct AttnSplit {
+  bool mixed;
+  AttnPlan dec;
+  AttnPlan pre;
+  size_t ws_bytes;
+};
+AttnSplit plan_split(int n_seq, int max_q_len, int hq, int hkv, int d, int max_blk,
+                     int block_size, int max_kv_len, int part_tokens, int dtype,
+                     bool has_qloc);
 
 int launch_attention(const AttnArgs& a, const AttnPlan& plan, int dtype,
                      hipStream_t stream);
