@@ -339,6 +339,16 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
     p.ws_bytes = sk_workspace_bytes(group, d);
     return p;
   }
+  if (max_q_len > 1 && max_blk >= 1 && prefill_mfma_supported(dtype, group, d)) {
+    // MFMA prefill: one workgroup per 128-row tile, whole causal range
+    p.kind = 3;
+    p.rows = 128;
+    p.tiles_max = 1;
+    p.part_tokens = 0;
+    p.parts_max = 1;
+    p.ws_bytes = 0;
+    return p;
+  }
   p.kind = mfma ? 1 : 0;
   p.rows = mfma ? group : kGenRows;
   p.tiles_max = ceil_div_h((int64_t)max_q_len * group, p.rows);
@@ -428,6 +438,7 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
     if (dtype == PKV_DTYPE_BF16) return launch_mfma<bf16>(a, p, dtype, stream);
     return launch_mfma<f16>(a, p, dtype, stream);
   }
+  if (p.kind == 3) return launch_prefill_mfma(a, dtype, stream);
   switch (dtype) {
     case PKV_DTYPE_F32: return launch_generic<float>(a, p, stream);
     case PKV_DTYPE_F16: return launch_generic<f16>(a, p, stream);

@@ -211,8 +211,8 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
   if (!sp.mixed) {
     AttnArgs a = args_for(sp.dec, 0);
     if (k_new) {
-      if (sp.dec.kind == 0) {
-        // no fused form for the generic kernel: append, then attend
+      if (sp.dec.kind == 0 || sp.dec.kind == 3) {
+        // the fused form is the decode kernels': append, then attend
         const int rc = launch_append_from_table(
             const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
             v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens,

@@ -120,7 +120,7 @@ inline size_t sk_workspace_bytes(int group, int d) {
 
 struct AttnPlan {
   int kind;        // 0 = generic rows kernel, 1 = MFMA partition kernel,
-                   // 2 = MFMA persistent kernel
+                   // 2 = MFMA persistent kernel, 3 = MFMA prefill kernel
   int rows;        // rows per tile of the chosen kernel
   int part_tokens;
   int parts_max;
@@ -209,6 +209,12 @@ int launch_attention(const AttnArgs& a, const AttnPlan& plan, int dtype,
 // group 16 or 32, head dim 64 or 128.
 bool decode_mfma_supported(int dtype, int max_q_len, int group, int d);
 bool pool_needs_off64(const AttnArgs& a);
+
+// MFMA prefill / chunked-prefill kernel (prefill_mfma.hip): bf16/fp16, query
+// runs of any length (query_start_loc required), group 16 or 32, head dim
+// 64 or 128.
+bool prefill_mfma_supported(int dtype, int group, int d);
+int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t stream);
 int launch_decode_mfma(const AttnArgs& a, const AttnPlan& plan, int dtype,
                        hipStream_t stream);
 // Persistent MFMA decode kernel (decode_sk.hip), same coverage.

@@ -120,7 +120,7 @@ def decode_problem(lens, hq, hkv, d, bs, num_blocks, dtype, device, seed,
     if garbage is not None:
         owned = torch.zeros(num_blocks * bs, dtype=torch.bool, device=device)
         for t, n in zip(tables, lens):
-            idx = (torch.as_tensor(t, device=device)[:, None] * bs
+            idx = (torch.as_tensor(t, device=device, dtype=torch.long)[:, None] * bs
                    + torch.arange(bs, device=device)).reshape(-1)[:int(n)]
             owned[idx] = True
         k_pool.view(-1, hkv, d)[~owned] = garbage
