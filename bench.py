@@ -23,6 +23,8 @@ Printed JSON line:
                time from HIP events on its stream, against 8 TB/s;
   north_star   the same kernel on config 5 (Hq 32, D 128, batch 256,
                lognormal context mean 1024, fragmented tables);
+  cfg5_mixed_step  config 5's whole step: those 256 decodes plus a
+               chunked-prefill append of 4 new sequences, one fused call;
   cpu_baseline the reference's PyTorch path (index_select gather + SDPA,
                the oracle) on this host's cores, on a bounded sample.
 """
@@ -232,6 +234,51 @@ def run_north_star(args, torch):
             "frac_of_peak": gbs / HBM_PEAK_GBS, "target_frac": 0.70}
 
 
+def mixed_step_bytes(dec_lens, chunk, n_new, hq=32, d=128, esize=2, bs=16):
+    """Algorithmic bytes of one config-5 mixed step: every visible K/V row
+    read once (decode contexts after the append, each new sequence's chunk),
+    Q in and O out for every query token, the appended K/V rows read and
+    written, 4 B per block-table entry used and per seq_len."""
+    dec_kv = [int(x) + 1 for x in dec_lens]
+    kv = sum(dec_kv) + n_new * chunk
+    T = len(dec_kv) + n_new * chunk
+    blocks = sum((x + bs - 1) // bs for x in dec_kv) + n_new * ((chunk + bs - 1) // bs)
+    return (kv * d * 2 * esize + 2 * T * hq * d * esize + 4 * T * d * esize
+            + 4 * blocks + 4 * (len(dec_kv) + n_new))
+
+
+def run_mixed_step(args, torch):
+    """Config 5 as BASELINE defines its step: the 256 decode queries and a
+    chunked-prefill append for 4 new sequences (4 x 128 tokens; 4 x 512 also
+    reported), one fused append + attention call (bs 16)."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_attention_append_meta
+
+    dev = torch.device("cuda:0")
+    res = {}
+    for chunk in (128, 512):
+        p = workloads.cfg5_mixed_problem(dev, chunk=chunk, seed=0, bs=16)
+        out = torch.empty_like(p.q)
+
+        def step():
+            paged_attention_append_meta(p.q, p.k, p.v, p.pool, 0, p.meta, out=out)
+        for _ in range(5):
+            step()
+        sec = time_events(step, 50, torch.cuda.current_stream(dev))
+        nbytes = mixed_step_bytes(p.dec_lens, chunk, p.n_new)
+        gbs = nbytes / sec / 1e9
+        log(f"cfg5 mixed step (256 decode + 4 x {chunk} prefill): {sec * 1e6:.1f} us, "
+            f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
+        res[f"prefill_{chunk}"] = {"us_per_step": round(sec * 1e6, 2), "bytes_per_step": nbytes,
+                                   "achieved_gbs": round(gbs, 1),
+                                   "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    res["workload"] = ("cfg5 step: 256 decode queries (lognormal ctx mean 1024 cap 8192, seed 0) "
+                       "each appending one token, plus a chunked-prefill append of 4 new "
+                       "sequences (4 x 128, and 4 x 512), bf16, Hq 32, Hkv 1, D 128, bs 16, "
+                       "fragmented tables; one fused append + attention call")
+    return res
+
+
 def run_cpu_baseline(hot, torch):
     """The reference's PyTorch paged path (oracle.torch_ref: per-sequence
     index_select gather + scaled_dot_product_attention, as in the
@@ -277,7 +324,15 @@ def run_profile(args, torch):
     from serving.paged_meta import pack_batch_meta
 
     dev = torch.device("cuda:0")
-    if args.profile == "cfg4":
+    if args.profile == "cfg5mixed":
+        p = workloads.cfg5_mixed_problem(dev, chunk=128, seed=0, bs=16)
+        out = torch.empty_like(p.q)
+        from serving.fake_paged_attn import paged_attention_append_meta
+
+        def attn():
+            paged_attention_append_meta(p.q, p.k, p.v, p.pool, 0, p.meta, out=out)
+        nbytes = mixed_step_bytes(p.dec_lens, 128, p.n_new)
+    elif args.profile == "cfg4":
         L, N, HQ, HKV, D, BS, NB = 1, 128, 16, 1, 64, 16, 16384
         lens = workloads.lengths_uniform(N, 256, 2048, seed=0)
         tables = cfg4_tables(lens, BS, NB, 1, seed=0)
@@ -324,7 +379,7 @@ def main():
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
-    ap.add_argument("--profile", choices=["cfg4", "cfg5"], default=None,
+    ap.add_argument("--profile", choices=["cfg4", "cfg5", "cfg5mixed"], default=None,
                     help="run only the decode-attention launches of this workload "
                          "(a rocprofv3 target); no JSON line")
     ap.add_argument("--profile-iters", type=int, default=20)
@@ -352,6 +407,7 @@ def main():
     value = hot["step_bytes"] / hot["step_sec"] / 1e9
     model = None if args.no_model else run_model(args, torch)
     ns = None if args.no_north_star else run_north_star(args, torch)
+    mixed = None if args.no_north_star else run_mixed_step(args, torch)
     cpu = None if args.no_cpu else run_cpu_baseline(hot, torch)
 
     achieved = hot["attn_bytes"] / hot["attn_sec"] / 1e9
@@ -409,6 +465,7 @@ def main():
             "us_per_launch": round(hot["attn_sec"] * 1e6, 3),
         },
         "north_star": ns,
+        "cfg5_mixed_step": mixed,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -166,13 +166,15 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
  * pkv_append_from_table followed by pkv_paged_attention in one call: the
  * step's new K/V rows (k_new, v_new [n_tokens, hkv, d], row t of sequence s
  * at position start_pos[s] + t - query_start_loc[s]) are appended to the
- * pools and attended to by the same launch. On the MFMA decode kernels
- * (bf16/f16, one query per sequence, 16 or 32 query heads per kv head,
- * d = 64 or 128) the append is fused into the attention: the workgroup
- * whose context range covers the new row takes it from k_new / v_new and
- * the one holding the sequence's last chunk writes it to its pool slot;
- * elsewhere the two steps run back to back. Same results, status bits
- * and pool contents as the two calls. query_start_loc is required.
+ * pools and attended to by the same call. On the split-K partition decode
+ * kernel (bf16/f16, one query per sequence, 16 or 32 query heads per kv
+ * head, d = 64 or 128, context bound below 4096 tokens) the append is fused
+ * into the attention launch: the workgroup whose context range covers the
+ * new row takes it from k_new / v_new and the one holding the sequence's
+ * last chunk writes it to its pool slot; elsewhere (persistent decode,
+ * prefill and mixed batches' prefill rows, generic kernel) the table append
+ * runs first. Same results, status bits and pool contents as the two calls.
+ * query_start_loc is required.
  * Replaces KVPool.write + paged_varlen_attention as called per layer in
  * MQA_Paged.forward_paged_batched (serving/paged_mqa.py:98-110).
  */

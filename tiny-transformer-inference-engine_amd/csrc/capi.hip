@@ -208,11 +208,15 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     return a;
   };
   const int64_t row_bytes = (int64_t)hkv * d * elem_bytes(dtype);
+  // Only the split-K partition decode kernel takes the append fused: for
+  // the persistent kernel the fused form measured slower than a separate
+  // append launch (register pressure at 32 heads x 128 dims), and the
+  // prefill and generic kernels read every row from the pool.
   if (!sp.mixed) {
     AttnArgs a = args_for(sp.dec, 0);
     if (k_new) {
-      if (sp.dec.kind == 0 || sp.dec.kind == 3) {
-        // the fused form is the decode kernels': append, then attend
+      if (sp.dec.kind != 1) {
+        // append, then attend
         const int rc = launch_append_from_table(
             const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
             v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens,
@@ -226,20 +230,23 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     }
     return launch_attention(a, sp.dec, dtype, (hipStream_t)stream);
   }
-  // mixed batch: the decode sequences on an MFMA decode kernel (with their
-  // append fused), then the prefill sequences, whose rows are appended
-  // first because the prefill kernel reads them from the pool
+  // mixed batch: the decode sequences on an MFMA decode kernel, then the
+  // prefill sequences; the prefill rows (and the decode rows unless the
+  // decode kernel takes them fused) are appended first
   AttnArgs ad = args_for(sp.dec, 1);
   const AttnArgs ap = args_for(sp.pre, 2);
   if (k_new) {
+    const bool fuse = sp.dec.kind == 1;
     const int rc = launch_append_from_table(
         const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
         v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens, row_bytes,
-        2, status, (hipStream_t)stream);
+        fuse ? 2 : 0, status, (hipStream_t)stream);
     if (rc != PKV_OK) return rc;
-    ad.k_new = k_new;
-    ad.v_new = v_new;
-    ad.new_pos = start_pos;
+    if (fuse) {
+      ad.k_new = k_new;
+      ad.v_new = v_new;
+      ad.new_pos = start_pos;
+    }
   }
   int rc = launch_attention(ad, sp.dec, dtype, (hipStream_t)stream);
   if (rc != PKV_OK) return rc;

@@ -123,7 +123,7 @@ __device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
   return __builtin_amdgcn_readfirstlane(total);
 }
 
-template <typename T, int D, int NT, int PF, bool OFF64, bool APP>
+template <typename T, int D, int NT, int PF, bool OFF64>
 __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs k) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -139,7 +139,6 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   __shared__ int tbl[kTblCap];
   __shared__ int scan_sh[kBlock];
   __shared__ int s_v0, s_g0;
-  __shared__ __attribute__((aligned(16))) char new_lds[2 * Geo::ROW_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -257,21 +256,9 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       nkl = ld_meta(a.seq_lens, sn);
     }
 
-    // fused append: this share stages the new row when it covers its
-    // position, and writes it into the pool when it holds the last chunk
-    NewRow nr;
+    NewRow nr;  // no appended row: the library appends before this kernel
     nr.pos = -1;
-    nr.lds = new_lds;
-    int new_pos = -1;
-    bool new_write = false, new_pending = false;  // pending: row buffer still to fill
-    if constexpr (APP) {
-      new_pos = a.new_pos[s];
-      const bool new_here = new_pos >= tok_lo && new_pos < tok_hi;
-      new_write = c1 == n;
-      if (new_here) nr.pos = new_pos;
-      new_pending = (new_here || new_write) && !prestaged;
-    }
-    int last_blk_lo = 0, last_nblk = 0;
+    nr.lds = nullptr;
     pv.head_off = (int64_t)kvh * D * 2;
     const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
     WaveState<NT, DT> st;
@@ -281,32 +268,17 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       cx.seg_hi = min(lo + win, tok_hi);
       cx.blk_lo = lo >> a.bs_shift;
       const int nblk = ((cx.seg_hi - 1) >> a.bs_shift) + 1 - cx.blk_lo;
-      __syncthreads();  // previous window's table / slices / row buffer no longer read
-      if (prestaged && lo == tok_lo) {
-        // staged during the previous segment's merge
-      } else if (APP && new_pending) {
-        // the new row's load is in flight with the table slice's
-        const u32x4 piece = load_new_row<D>(a, qtok, kvh, tid);
-        for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
-        put_new_row<D>(new_lds, piece, tid);
-        new_pending = false;
-      } else {
+      __syncthreads();  // previous window's table and slices no longer read
+      if (!(prestaged && lo == tok_lo)) {  // else staged during the previous segment's merge
         for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
       }
       __syncthreads();
-      run_chunks<T, D, NT, PF, OFF64, APP>(w, kWaves, cx, pv, qf, st, bad_block, nr);
-      last_blk_lo = cx.blk_lo;
-      last_nblk = nblk;
-    }
-    if (APP && new_write) {
-      if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, qtok, kvh, tid), tid);
-      // each thread stores the piece it put into the buffer itself
-      store_new_row<D>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk, tid);
+      run_chunks<T, D, NT, PF, OFF64, false>(w, kWaves, cx, pv, qf, st, bad_block, nr);
     }
 
     // ---- the next segment: its Q and first table window are loaded now
-    // (qf is free once this segment has streamed; the table and row buffer
-    // are written to LDS after the merge)
+    // (qf is free once this segment has streamed; the table is written to
+    // LDS after the merge)
     int v_n = v + 1;
     const int g0_n = g0 + n + K;
     SeqDesc d_n = seq_desc(a, nq0, nq1, nkl);
@@ -332,13 +304,6 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     // max_blk >= 1 for this kernel: entry 0 of the row is always readable
     const int tpref =
         a.block_tables[(int64_t)s_n * a.max_blk + max(0, min(tid, n_nblk - 1))];
-    bool n_row = false;
-    u32x4 n_piece = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (APP) {
-      const int pos_n = a.new_pos[s_n];
-      n_row = has_next && ((pos_n >= 0 && pos_n < tok_hi_n) || c1_n == d_n.n);
-      n_piece = load_new_row<D>(a, qtok_n, kvh_n, tid);
-    }
 
     // ---- merge the wavefronts' states through LDS ----
 #pragma unroll
@@ -408,9 +373,6 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     __syncthreads();  // LDS merge area, table and row buffer are free
     if (!has_next) break;
     if (tid < n_nblk) tbl[tid] = tpref;  // published by the window loop's first barrier
-    if constexpr (APP) {
-      if (n_row) put_new_row<D>(new_lds, n_piece, tid);
-    }
     prestaged = true;
     v = v_n;
     g0 = g0_n;
@@ -483,12 +445,8 @@ __global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArg
 template <typename T, int D, int NT, int PF, bool OFF64>
 int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
   k.n_wg = sk_workgroups(D, 16 * NT);
-  if (a.new_pos)
-    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, true>), dim3(k.n_wg), dim3(kBlock),
-                       0, stream, a, k);
-  else
-    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, false>), dim3(k.n_wg),
-                       dim3(kBlock), 0, stream, a, k);
+  hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64>), dim3(k.n_wg), dim3(kBlock), 0,
+                     stream, a, k);
   int rc = check_launch("decode_sk_kernel");
   if (rc != PKV_OK) return rc;
   constexpr int G = 16 * NT;
@@ -500,8 +458,7 @@ int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
 template <typename T, bool OFF64>
 int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
   const int nt = a.group / 16;
-  // <T, D, NT, PF, OFF64>: two wavefronts per SIMD, with and without the
-  // fused append (APP); the D = 128 variants
+  // <T, D, NT, PF, OFF64>: two wavefronts per SIMD; the D = 128 variants
   // have room for one chunk in flight per wavefront, the D = 64 ones for two
   if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, OFF64>(a, k, stream);
   if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, OFF64>(a, k, stream);

@@ -148,3 +148,45 @@ def cfg5_problem(device, seed=0, bs=16, dtype=torch.bfloat16):
     num_blocks = 1 << max(10, math.ceil(math.log2(need * 1.6 + 1)))
     return decode_problem(lens, 32, 1, 128, bs, num_blocks, dtype, device, seed,
                           fragmented=True)
+
+
+@dataclass
+class MixedProblem:
+    pool: object      # KVPool (one layer)
+    meta: object      # PagedBatchMeta of the step
+    q: torch.Tensor   # [T, 32, 128]
+    k: torch.Tensor   # [T, 1, 128] rows appended this step
+    v: torch.Tensor
+    dec_lens: np.ndarray  # decode contexts before the step
+    chunk: int
+    n_new: int
+
+
+def cfg5_mixed_problem(device, chunk=128, n_new=4, seed=0, bs=16, dtype=torch.bfloat16):
+    """One config-5 step: the 256 decode sequences (lognormal contexts) each
+    append one token and attend over it, and n_new new sequences append and
+    attend over their first `chunk` prompt tokens (chunked prefill), in one
+    batch; tables fragmented as in cfg5_problem, from one allocator."""
+    from .kv_pool import KVPool
+    from .paged_meta import pack_batch_meta
+
+    dec = lengths_lognormal(256, 1024, 8192, seed)
+    starts = [int(x) for x in dec] + [0] * n_new
+    q_lens = [1] * len(dec) + [chunk] * n_new
+    ends = [s + q for s, q in zip(starts, q_lens)]
+    need = int(sum((e + bs - 1) // bs for e in ends))
+    num_blocks = 1 << max(10, math.ceil(math.log2(need * 1.6 + 1)))
+    tables = fragmented_tables(ends, bs, num_blocks, seed)
+    dev = torch.device(device)
+    pool = KVPool(1, bs, num_blocks, 1, 128, dtype, dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pool.kv.normal_(generator=g)
+    T = sum(q_lens)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
+    positions = [p for s, q in zip(starts, q_lens) for p in range(s, s + q)]
+    meta = pack_batch_meta(tables, qsl, positions, T, dev, bs)
+    q = torch.randn(T, 32, 128, generator=g, device=dev).to(dtype)
+    k = torch.randn(T, 1, 128, generator=g, device=dev).to(dtype)
+    v = torch.randn(T, 1, 128, generator=g, device=dev).to(dtype)
+    return MixedProblem(pool=pool, meta=meta, q=q, k=k, v=v, dec_lens=dec, chunk=chunk,
+                        n_new=n_new)
