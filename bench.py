@@ -324,6 +324,12 @@ def run_profile(args, torch):
     from serving.paged_meta import pack_batch_meta
 
     dev = torch.device("cuda:0")
+    if args.profile == "model":
+        # the config-4 model decode step, replayed from its HIP graph
+        args.model_steps = args.profile_iters
+        args.warmup = 1
+        run_model(args, torch)
+        return
     if args.profile == "cfg5mixed":
         p = workloads.cfg5_mixed_problem(dev, chunk=128, seed=0, bs=16)
         out = torch.empty_like(p.q)
@@ -379,7 +385,7 @@ def main():
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
-    ap.add_argument("--profile", choices=["cfg4", "cfg5", "cfg5mixed"], default=None,
+    ap.add_argument("--profile", choices=["cfg4", "cfg5", "cfg5mixed", "model"], default=None,
                     help="run only the decode-attention launches of this workload "
                          "(a rocprofv3 target); no JSON line")
     ap.add_argument("--profile-iters", type=int, default=20)

@@ -32,6 +32,13 @@
  *                         split-K and therefore no workspace.
  *   pkv_paged_attention_append  KVPool.write + paged_varlen_attention per
  *                         layer                      serving/paged_mqa.py:98-110
+ *   pkv_rms_norm          RMSNorm.forward            models/rmsnorm.py:12-18
+ *                         (with the residual add of PagedBlock.forward,
+ *                         serving/paged_model.py:20-29, fused in front)
+ *   pkv_rope              RoPE.forward_at / _rotate  models/rope.py:21-47
+ *                         as applied to q, k in MQA_Paged.forward_paged_batched
+ *                                                    serving/paged_mqa.py:80-85
+ *   pkv_silu_mul          fused_swiglu               kernels/fused_swiglu/kernel.py:6-19,131-136
  */
 #ifndef PAGEDKV_H
 #define PAGEDKV_H
@@ -66,6 +73,7 @@ extern "C" {
                                     (or block 0 for an append) was skipped */
 #define PKV_STATUS_SHORT_TABLE 4 /* append: position beyond the table      */
 #define PKV_STATUS_BAD_QLOC 8    /* attention: query range outside [0, T)  */
+#define PKV_STATUS_BAD_POS 16    /* rope: position outside [0, max_pos)    */
 
 /* Library version (PKV_VERSION). */
 int pkv_version(void);
@@ -190,6 +198,54 @@ int pkv_paged_attention_append(void* out, float* lse, const void* q,
                                const void* v_new, const int32_t* start_pos,
                                void* workspace, size_t workspace_bytes,
                                int* status, void* stream);
+
+/*
+ * RMSNorm over rows of `dim` elements: y = (x * rsqrt(mean(x^2) + eps)) * w,
+ * computed in fp32 and rounded once to `dtype` (weight has `dtype` too).
+ * With `delta` non-null, the residual sum r = x + delta (rounded to `dtype`)
+ * is written to residual_out (which may be x itself when x_stride == dim)
+ * and normalised instead of x. x and delta rows are x_stride / delta_stride
+ * elements apart; y and residual_out are contiguous [rows, dim].
+ * Replaces RMSNorm.forward (models/rmsnorm.py:12-18) and the residual add
+ * before it (serving/paged_model.py:20-29).
+ */
+int pkv_rms_norm(void* y, void* residual_out, const void* x, const void* delta,
+                 const void* weight, int64_t rows, int dim, int64_t x_stride,
+                 int64_t delta_stride, float eps, int dtype, void* stream);
+
+/*
+ * Rotary embedding of one step's token-major rows, interleaved (even, odd)
+ * pairs, at absolute positions[t] (int32 [n_tokens]):
+ *   out[2i]   = x[2i] * cos - x[2i+1] * sin
+ *   out[2i+1] = x[2i] * sin + x[2i+1] * cos,  cos/sin = table[pos][i]
+ * q rows (hq heads of d) start q_stride elements apart, k rows (hkv heads)
+ * k_stride apart, so q, k and v may be column ranges of one fused
+ * projection output; q_out [n_tokens, hq, d] and k_out [n_tokens, hkv, d]
+ * are written contiguous. With v non-null, v's rows (v_stride apart) are
+ * copied to a contiguous v_out [n_tokens, hkv, d] in the same launch.
+ * cos_table / sin_table: fp32 [max_pos, d/2]; their values are rounded to
+ * `dtype` and every product and sum is rounded to `dtype`, as in the
+ * framework's element-wise evaluation (bit-exact in fp32: no fused
+ * multiply-add). A position outside [0, max_pos) sets PKV_STATUS_BAD_POS in
+ * `status` (nullable) and rotates by angle 0.
+ * Replaces RoPE.forward_at / _rotate (models/rope.py:21-47) as applied in
+ * MQA_Paged.forward_paged_batched (serving/paged_mqa.py:80-85).
+ */
+int pkv_rope(void* q_out, void* k_out, void* v_out, const void* q, const void* k,
+             const void* v, int64_t q_stride, int64_t k_stride, int64_t v_stride,
+             const int32_t* positions, const float* cos_table, const float* sin_table,
+             int max_pos, int64_t n_tokens, int hq, int hkv, int d, int dtype,
+             int* status, void* stream);
+
+/*
+ * SwiGLU gate: out = gate * sigmoid(gate) * up in fp32, rounded once to
+ * `dtype`. gate / up rows are gate_stride / up_stride elements apart (they
+ * may be the two halves of one fused projection output); out is contiguous
+ * [rows, cols]. Replaces fused_swiglu (kernels/fused_swiglu/kernel.py:6-19,
+ * :131-136).
+ */
+int pkv_silu_mul(void* out, const void* gate, const void* up, int64_t rows, int64_t cols,
+                 int64_t gate_stride, int64_t up_stride, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

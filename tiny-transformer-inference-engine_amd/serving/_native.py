@@ -21,6 +21,7 @@ PKV_STATUS_BAD_SLOT = 1
 PKV_STATUS_BAD_BLOCK = 2
 PKV_STATUS_SHORT_TABLE = 4
 PKV_STATUS_BAD_QLOC = 8
+PKV_STATUS_BAD_POS = 16
 # part_tokens value selecting the persistent (stream-K) decode kernel
 PART_PERSISTENT = -1
 
@@ -56,6 +57,13 @@ _SIGNATURES = {
                                     _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
                                     _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_size,
                                     _c_vp, _c_vp], _c_int),
+    "pkv_rms_norm": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_i64, _c_i64,
+                      _c_float, _c_int, _c_vp], _c_int),
+    "pkv_rope": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp,
+                  _c_vp, _c_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp],
+                 _c_int),
+    "pkv_silu_mul": ([_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp],
+                     _c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

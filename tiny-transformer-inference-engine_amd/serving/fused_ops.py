@@ -1,0 +1,207 @@
+"""Host wrappers of the decoder block's element-wise kernels in libpagedkv.so
+(csrc/layers.hip): RMSNorm with a fused residual add, RoPE on token-major
+Q/K rows (optionally split out of one fused projection output), and the
+SwiGLU gate.
+
+Every function requires ROCm device tensors and the library; there is no
+framework fallback (RuntimeError otherwise). Outputs are allocated with
+torch on the input's device and the current stream, so the calls can be
+captured in a HIP graph.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+
+def _rows(x: torch.Tensor, what: str):
+    """x viewed as [rows, dim] with unit column stride: (tensor, rows, stride)."""
+    if x.dim() == 0:
+        raise ValueError(f"{what}: expected at least one dimension")
+    dim = x.shape[-1]
+    x2 = x.reshape(-1, dim) if x.dim() != 2 else x
+    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < dim):
+        x2 = x2.contiguous()
+    return x2, x2.shape[0], (x2.stride(0) if x2.shape[0] > 1 else dim)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm of the last dimension: (x * rsqrt(mean(x^2) + eps)) * weight in
+    fp32, rounded to x.dtype (models/rmsnorm.py:12-18)."""
+    _native.require_device(x, weight, what="rms_norm")
+    w = weight if weight.dtype == x.dtype else weight.to(x.dtype)
+    w = w.contiguous()
+    if w.numel() != x.shape[-1]:
+        raise ValueError(f"rms_norm: weight has {w.numel()} elements, rows have {x.shape[-1]}")
+    x2, rows, stride = _rows(x, "rms_norm")
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    rc = _native.lib().pkv_rms_norm(
+        y.data_ptr(), None, x2.data_ptr(), None, w.data_ptr(), rows, x.shape[-1], stride,
+        0, float(eps), _native.dtype_code(x.dtype), _native.stream_ptr(x.device))
+    _native.check(rc, "rms_norm")
+    return y
+
+
+def add_rms_norm_(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor,
+                  eps: float) -> torch.Tensor:
+    """x += delta (rounded to x.dtype, in place), then return rms_norm(x):
+    the residual add of a decoder block fused with the next norm
+    (serving/paged_model.py:20-29). x must be contiguous."""
+    _native.require_device(x, delta, weight, what="add_rms_norm_")
+    if not x.is_contiguous():
+        raise ValueError("add_rms_norm_: x must be contiguous (it is updated in place)")
+    if delta.shape != x.shape or delta.dtype != x.dtype:
+        raise ValueError(f"add_rms_norm_: delta {tuple(delta.shape)} {delta.dtype} vs x "
+                         f"{tuple(x.shape)} {x.dtype}")
+    w = weight if weight.dtype == x.dtype else weight.to(x.dtype)
+    w = w.contiguous()
+    dim = x.shape[-1]
+    if w.numel() != dim:
+        raise ValueError(f"add_rms_norm_: weight has {w.numel()} elements, rows have {dim}")
+    d2, rows, dstride = _rows(delta, "add_rms_norm_")
+    y = torch.empty_like(x)
+    rc = _native.lib().pkv_rms_norm(
+        y.data_ptr(), x.data_ptr(), x.data_ptr(), d2.data_ptr(), w.data_ptr(), rows, dim, dim,
+        dstride, float(eps), _native.dtype_code(x.dtype), _native.stream_ptr(x.device))
+    _native.check(rc, "add_rms_norm_")
+    return y
+
+
+def _tok_rows(t: torch.Tensor, heads: int, d: int, what: str):
+    """[T, heads, d] or [T, heads*d] rows with contiguous heads: (tensor, row stride)."""
+    if t.dim() == 3:
+        if t.shape[1] != heads or t.shape[2] != d:
+            raise ValueError(f"{what}: expected [T, {heads}, {d}], got {tuple(t.shape)}")
+        ok = t.stride(2) == 1 and t.stride(1) == d
+        if not ok:
+            t = t.contiguous()
+        return t, (t.stride(0) if t.shape[0] > 1 else heads * d)
+    if t.dim() == 2 and t.shape[1] == heads * d:
+        if t.stride(1) != 1:
+            t = t.contiguous()
+        return t, (t.stride(0) if t.shape[0] > 1 else heads * d)
+    raise ValueError(f"{what}: expected [T, {heads}, {d}], got {tuple(t.shape)}")
+
+
+def rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+         sin: torch.Tensor, v: torch.Tensor | None = None, hq: int | None = None,
+         hkv: int | None = None, d: int | None = None):
+    """Rotary embedding of q [T, Hq, D] and k [T, Hkv, D] at positions [T]
+    with fp32 tables cos/sin [max_pos, D/2] (models/rope.py:21-47, values and
+    intermediate products rounded to q.dtype). q, k (and v) may be strided
+    column ranges of one projection output, given as [T, H*D] slices with
+    hq/hkv/d. Returns contiguous (q_rot, k_rot) or, with v, (q_rot, k_rot,
+    v_contiguous)."""
+    if q.dim() == 3:
+        hq, d = q.shape[1], q.shape[2]
+    if k.dim() == 3:
+        hkv = k.shape[1]
+    if hq is None or hkv is None or d is None:
+        raise ValueError("rope: pass hq, hkv and d for 2-D q / k")
+    tensors = [q, k, positions, cos, sin] + ([v] if v is not None else [])
+    _native.require_device(*tensors, what="rope")
+    if k.dtype != q.dtype or (v is not None and v.dtype != q.dtype):
+        raise ValueError("rope: q, k, v must share a dtype")
+    T = q.shape[0]
+    if k.shape[0] != T or (v is not None and v.shape[0] != T) or positions.numel() != T:
+        raise ValueError("rope: q, k, v and positions disagree on the token count")
+    cos2 = cos.reshape(-1, d // 2)
+    sin2 = sin.reshape(-1, d // 2)
+    if cos2.dtype != torch.float32 or sin2.dtype != torch.float32 or cos2.shape != sin2.shape:
+        raise ValueError("rope: cos / sin must be fp32 tables of equal shape [max_pos, D/2]")
+    cos2, sin2 = cos2.contiguous(), sin2.contiguous()
+    pos = positions if positions.dtype == torch.int32 else positions.to(torch.int32)
+    pos = pos.contiguous()
+    qs, q_stride = _tok_rows(q, hq, d, "rope q")
+    ks, k_stride = _tok_rows(k, hkv, d, "rope k")
+    q_out = torch.empty((T, hq, d), dtype=q.dtype, device=q.device)
+    k_out = torch.empty((T, hkv, d), dtype=q.dtype, device=q.device)
+    if v is not None:
+        vs, v_stride = _tok_rows(v, hkv, d, "rope v")
+        v_out = torch.empty((T, hkv, d), dtype=q.dtype, device=q.device)
+    else:
+        vs, v_stride, v_out = None, 0, None
+    rc = _native.lib().pkv_rope(
+        q_out.data_ptr(), k_out.data_ptr(), _native.ptr(v_out), qs.data_ptr(), ks.data_ptr(),
+        _native.ptr(vs), q_stride, k_stride, v_stride, pos.data_ptr(), cos2.data_ptr(),
+        sin2.data_ptr(), cos2.shape[0], T, hq, hkv, d, _native.dtype_code(q.dtype), None,
+        _native.stream_ptr(q.device))
+    _native.check(rc, "rope")
+    return (q_out, k_out) if v is None else (q_out, k_out, v_out)
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """gate * sigmoid(gate) * up in fp32, rounded once
+    (kernels/fused_swiglu/kernel.py:6-19). gate and up may be strided column
+    ranges of one [rows, 2H] projection output; the result is contiguous."""
+    _native.require_device(gate, up, what="silu_mul")
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError("silu_mul: gate and up must have the same shape and dtype")
+    g2, rows, gs = _rows(gate, "silu_mul")
+    u2, _, us = _rows(up, "silu_mul")
+    cols = gate.shape[-1]
+    out = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+    rc = _native.lib().pkv_silu_mul(out.data_ptr(), g2.data_ptr(), u2.data_ptr(), rows, cols,
+                                    gs, us, _native.dtype_code(gate.dtype),
+                                    _native.stream_ptr(gate.device))
+    _native.check(rc, "silu_mul")
+    return out
+
+
+class FusedRows:
+    """Row-concatenated weights (and biases) of several nn.Linear modules
+    sharing an input, so one GEMM computes all of their outputs. The
+    modules' parameters are re-pointed to views of the concatenation, so
+    they stay the state-dict entries, in-place updates (load_state_dict,
+    optimiser steps) reach the fused storage, and no copy is kept. When a
+    parameter has been replaced (module.to(...), assignment) the
+    concatenation is rebuilt on the next call."""
+
+    def __init__(self, *linears: torch.nn.Linear):
+        self.linears = linears
+        self.weight = None
+        self.bias = None
+
+    def _views_intact(self) -> bool:
+        if self.weight is None:
+            return False
+        off = 0
+        base = self.weight.data_ptr()
+        es = self.weight.element_size()
+        for lin in self.linears:
+            w = lin.weight
+            if (w.device != self.weight.device or w.dtype != self.weight.dtype
+                    or w.data_ptr() != base + off * es or not w.is_contiguous()):
+                return False
+            off += w.numel()
+        if self.bias is not None:
+            off, base, es = 0, self.bias.data_ptr(), self.bias.element_size()
+            for lin in self.linears:
+                b = lin.bias
+                if b is None or b.data_ptr() != base + off * es or b.dtype != self.bias.dtype:
+                    return False
+                off += b.numel()
+        elif any(lin.bias is not None for lin in self.linears):
+            return False
+        return True
+
+    def get(self):
+        """(weight [sum(out), in], bias or None) of the concatenation."""
+        if not self._views_intact():
+            with torch.no_grad():
+                w = torch.cat([lin.weight.detach() for lin in self.linears], 0)
+                has_b = [lin.bias is not None for lin in self.linears]
+                if any(has_b) and not all(has_b):
+                    raise ValueError("FusedRows: either every linear has a bias or none")
+                b = (torch.cat([lin.bias.detach() for lin in self.linears], 0)
+                     if all(has_b) else None)
+                off = 0
+                for lin in self.linears:
+                    n = lin.weight.shape[0]
+                    lin.weight.data = w[off:off + n]
+                    if b is not None:
+                        lin.bias.data = b[off:off + n]
+                    off += n
+            self.weight, self.bias = w, b
+        return self.weight, self.bias

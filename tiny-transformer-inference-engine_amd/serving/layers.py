@@ -1,4 +1,4 @@
-"""Dense layers around the paged attention path (they stay PyTorch ops).
+"""Dense layers around the paged attention path.
 
 Each keeps the reference module's constructor, parameter names and
 arithmetic so that state dicts load unchanged and results match:
@@ -7,6 +7,10 @@ arithmetic so that state dicts load unchanged and results match:
   SwiGLU          models/mlp.py:17-32 (silu(gate) * up, then down)
   TokenEmbedding  models/embedding.py:5-15
   ModelConfig     models/model_config.py:8-41
+As in the reference, which routes CUDA tensors to its own kernels
+(models/rmsnorm.py:18, models/mlp.py:30), tensors on a ROCm device go to the
+HIP kernels of fused_ops (RMSNorm, token-major RoPE, the SwiGLU gate, with
+gate and up computed by one GEMM); CPU tensors use the PyTorch formulas.
 """
 from __future__ import annotations
 
@@ -15,6 +19,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+
+from . import fused_ops
 
 
 class RoPE(nn.Module):
@@ -33,6 +39,20 @@ class RoPE(nn.Module):
         # [1, 1, max_seq_len, dim/2], non-persistent like the reference
         self.register_buffer("cos", angles.cos()[None, None], persistent=False)
         self.register_buffer("sin", angles.sin()[None, None], persistent=False)
+
+    def _tables_fp32(self):
+        """cos / sin as fp32 [max_seq_len, dim/2] for the HIP kernel, which
+        rounds them to the activation dtype itself. A module moved to a
+        lower precision holds its tables in that precision already (rounded
+        once; rounding again changes nothing), so the fp32 copy is exact;
+        it is cached until the buffers change."""
+        key = (self.cos.data_ptr(), self.cos._version, self.sin.data_ptr(), self.sin._version)
+        if getattr(self, "_t32_key", None) != key:
+            half = self.dim // 2
+            self._t32 = (self.cos.float().reshape(-1, half).contiguous(),
+                         self.sin.float().reshape(-1, half).contiguous())
+            self._t32_key = key
+        return self._t32
 
     @staticmethod
     def _rotate(q, k, cos, sin):
@@ -56,9 +76,16 @@ class RoPE(nn.Module):
         sin = self.sin.index_select(2, positions).to(dtype=q.dtype)
         return self._rotate(q, k, cos, sin)
 
-    def forward_tokens(self, q, k, positions):
+    def forward_tokens(self, q, k, positions, v=None):
         """Token-major variant: q [T, Hq, D], k [T, Hkv, D]. Same element-wise
-        arithmetic as forward_at, without the head/token transposes."""
+        arithmetic as forward_at, without the head/token transposes. On a
+        ROCm device one HIP kernel rotates both (and, with v, also returns v
+        made contiguous: q, k, v may be strided slices of one projection)."""
+        if q.is_cuda:
+            cos, sin = self._tables_fp32()
+            return fused_ops.rope(q, k, positions, cos, sin, v=v)
+        if v is not None:
+            return (*self.forward_tokens(q, k, positions), v.contiguous())
         cos = self.cos[0, 0].index_select(0, positions).to(dtype=q.dtype)[:, None, :]
         sin = self.sin[0, 0].index_select(0, positions).to(dtype=q.dtype)[:, None, :]
         return self._rotate(q, k, cos, sin)
@@ -71,6 +98,8 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda:
+            return fused_ops.rms_norm(x, self.weight, self.eps)
         x32 = x.float()
         y = x32 * torch.rsqrt(x32.square().mean(dim=-1, keepdim=True) + self.eps)
         return (y * self.weight.float()).to(dtype=x.dtype)
@@ -83,7 +112,14 @@ class SwiGLU(nn.Module):
         self.up_proj = nn.Linear(d_model, hidden_dim, bias=bias)
         self.down_proj = nn.Linear(hidden_dim, d_model, bias=bias)
 
+        self._gate_up = fused_ops.FusedRows(self.gate_proj, self.up_proj)
+
     def forward(self, x):
+        if x.is_cuda:
+            w, b = self._gate_up.get()
+            gu = F.linear(x, w, b)
+            h = self.gate_proj.out_features
+            return self.down_proj(fused_ops.silu_mul(gu[..., :h], gu[..., h:]))
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 

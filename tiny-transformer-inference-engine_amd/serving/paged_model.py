@@ -11,6 +11,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
+from . import fused_ops
 from .layers import ModelConfig, RMSNorm, SwiGLU, TokenEmbedding
 from .paged_meta import pack_batch_meta
 from .paged_mqa import MQA_Paged
@@ -63,12 +64,30 @@ class PagedTransformer(nn.Module):
 
     @torch.no_grad()
     def forward_step(self, input_ids, pool, meta):
-        """forward_batch with pre-packed metadata (PagedBatchMeta)."""
+        """forward_batch with pre-packed metadata (PagedBatchMeta).
+
+        On a ROCm device every residual add runs inside the norm that
+        follows it (fused_ops.add_rms_norm_: x += delta, then normalise x),
+        so a layer is: norm, qkv GEMM, RoPE, append + attention, out GEMM,
+        add + norm, gate/up GEMM, SwiGLU gate, down GEMM. The arithmetic is
+        that of PagedBlock.forward_meta: each sum is rounded to the model
+        dtype before it is normalised or carried on."""
         x = self.embedding(input_ids)
-        for layer in self.layers:
-            x = layer.forward_meta(x, pool, meta)
         last = meta.query_start_loc[1:].long() - 1
-        return self.lm_head(self.final_norm(x.index_select(0, last)))
+        if not x.is_cuda:
+            for layer in self.layers:
+                x = layer.forward_meta(x, pool, meta)
+            return self.lm_head(self.final_norm(x.index_select(0, last)))
+        norms = [layer.attn_norm for layer in self.layers] + [self.final_norm]
+        h = norms[0](x)
+        for i, layer in enumerate(self.layers):
+            a = layer.attn.forward_meta(h, pool, layer.layer_idx, meta)
+            h = fused_ops.add_rms_norm_(x, a, layer.mlp_norm.weight, layer.mlp_norm.eps)
+            m = layer.mlp(h)
+            h = fused_ops.add_rms_norm_(x, m, norms[i + 1].weight, norms[i + 1].eps)
+        if not meta.is_decode:
+            h = h.index_select(0, last)
+        return self.lm_head(h)
 
 
 def load_paged_model(ckpt_path, device):
