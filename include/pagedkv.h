@@ -39,6 +39,12 @@
  *                         as applied to q, k in MQA_Paged.forward_paged_batched
  *                                                    serving/paged_mqa.py:80-85
  *   pkv_silu_mul          fused_swiglu               kernels/fused_swiglu/kernel.py:6-19,131-136
+ *   pkv_linear            nn.Linear of the block's out / down projections
+ *                                                    serving/paged_mqa.py:112-113,
+ *                                                    models/mlp.py:31-32
+ *   pkv_linear_swiglu     gate_proj, up_proj and fused_swiglu
+ *                                                    models/mlp.py:24-30
+ *   pkv_linear_rope_qkv   q/k/v projections and RoPE serving/paged_mqa.py:76-85
  */
 #ifndef PAGEDKV_H
 #define PAGEDKV_H
@@ -246,6 +252,48 @@ int pkv_rope(void* q_out, void* k_out, void* v_out, const void* q, const void* k
  */
 int pkv_silu_mul(void* out, const void* gate, const void* up, int64_t rows, int64_t cols,
                  int64_t gate_stride, int64_t up_stride, int dtype, void* stream);
+
+/*
+ * y = x W^T (+ bias) for few rows: x [m, k] (rows x_stride elements apart),
+ * W [n, k] contiguous, bias [n] (nullable), y [m, n] contiguous; bf16 / fp16
+ * storage, fp32 accumulation, one rounding. k must be a multiple of 32 and x
+ * rows 16-byte aligned (PKV_ERR_UNSUPPORTED otherwise, as for fp32). Built
+ * for decode steps (m up to a few hundred): the workgroups split k, so the
+ * weight is streamed by the whole chip. The sum order is fixed: results are
+ * deterministic and identical across the three pkv_linear* entry points.
+ * Replaces nn.Linear for the out projection (serving/paged_mqa.py:112-113)
+ * and down_proj (models/mlp.py:31-32).
+ */
+int pkv_linear(void* out, const void* x, const void* w, const void* bias, int64_t m, int64_t n,
+               int64_t k, int64_t x_stride, int dtype, void* stream);
+
+/*
+ * SwiGLU MLP front half: W = [gate rows; up rows] [2n, k] (bias [2n],
+ * nullable); out [m, n] = g * sigmoid(g) * u in fp32, rounded once, where g
+ * and u are the gate / up projections rounded to dtype (bit-identical to
+ * pkv_linear into [m, 2n] followed by pkv_silu_mul). Same requirements as
+ * pkv_linear. Replaces gate_proj, up_proj and fused_swiglu
+ * (models/mlp.py:24-30, kernels/fused_swiglu/kernel.py:6-19).
+ */
+int pkv_linear_swiglu(void* out, const void* x, const void* w_gate_up, const void* bias,
+                      int64_t m, int64_t n, int64_t k, int64_t x_stride, int dtype,
+                      void* stream);
+
+/*
+ * MQA_Paged's three projections and RoPE in one launch: W = [q rows; k rows;
+ * v rows] [(hq + 2 hkv) d, k] (bias nullable); q_out [m, hq, d] and k_out
+ * [m, hkv, d] receive the projections rotated at positions[m] (int32), v_out
+ * [m, hkv, d] the value projection; all contiguous. Bit-identical to
+ * pkv_linear into [m, (hq + 2 hkv) d] followed by pkv_rope on the three
+ * column ranges (same tables, same status bit for positions outside
+ * [0, max_pos)). Same requirements as pkv_linear. Replaces
+ * serving/paged_mqa.py:76-85.
+ */
+int pkv_linear_rope_qkv(void* q_out, void* k_out, void* v_out, const void* x, const void* w_qkv,
+                        const void* bias, int64_t m, int64_t k, int64_t x_stride,
+                        const int32_t* positions, const float* cos_table,
+                        const float* sin_table, int max_pos, int hq, int hkv, int d, int dtype,
+                        int* status, void* stream);
 
 #ifdef __cplusplus
 }

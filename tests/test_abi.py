@@ -80,3 +80,19 @@ def test_workspace_sizing():
     assert a > b > 0
     with pytest.raises(ValueError):
         _native.check(-1, "x")
+
+
+def test_linear_validation_without_gpu():
+    """Host-side rejections of the projection entry points (no launch)."""
+    L = _native.lib()
+    # fp32 is not taken (the library GEMM serves it), k must be a multiple of 32
+    assert L.pkv_linear(16, 16, 16, None, 4, 8, 64, 64, 0, None) == -2
+    assert L.pkv_linear(16, 16, 16, None, 4, 8, 40, 40, 2, None) == -2
+    assert L.pkv_linear(None, 16, 16, None, 4, 8, 64, 64, 2, None) == -1
+    assert L.pkv_linear(16, 16, 16, None, 4, 8, 64, 32, 2, None) == -1  # x_stride < k
+    assert L.pkv_linear_swiglu(16, 16, 16, None, 4, 8, 48, 48, 1, None) == -2
+    # odd head dim, missing tables
+    assert L.pkv_linear_rope_qkv(16, 16, 16, 16, 16, None, 4, 64, 64, 16, 16, 16, 8, 4, 1, 7,
+                                 2, None, None) == -1
+    assert L.pkv_linear_rope_qkv(16, 16, 16, 16, 16, None, 4, 64, 64, 16, None, 16, 8, 4, 1, 8,
+                                 2, None, None) == -1

@@ -57,7 +57,7 @@ __device__ __forceinline__ void st(T* p, const Pack<T, V>& r) {
 // value rounded to the storage type and back (identity for float)
 template <typename T>
 __device__ __forceinline__ float rnd(float x) {
-  return (float)(T)x;
+  return (float)(T)fp32_value(x);
 }
 
 struct RmsArgs {
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(64 * kRmsMaxWaves) void rms_norm_kernel(RmsArgs a) 
     if (h) {
       const Pack<T, V> hv = ld<T, V>(h + i);
 #pragma unroll
-      for (int e = 0; e < V; ++e) xv.e[e] = (T)((float)xv.e[e] + (float)hv.e[e]);
+      for (int e = 0; e < V; ++e) xv.e[e] = (T)fp32_value((float)xv.e[e] + (float)hv.e[e]);
       st<T, V>(r + i, xv);
     }
 #pragma unroll
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64 * kRmsMaxWaves) void rms_norm_kernel(RmsArgs a) 
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       const float n = (float)xv.e[e] * inv;
-      out.e[e] = (T)(n * (float)wv8.e[e]);
+      out.e[e] = (T)fp32_value(n * (float)wv8.e[e]);
     }
     st<T, V>(y + i, out);
   }
@@ -195,8 +195,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     const float sj = rnd<T>(sn[j]);
     const float xe = (float)xv.e[2 * j];
     const float xo = (float)xv.e[2 * j + 1];
-    out.e[2 * j] = (T)(rnd<T>(xe * cj) - rnd<T>(xo * sj));
-    out.e[2 * j + 1] = (T)(rnd<T>(xe * sj) + rnd<T>(xo * cj));
+    out.e[2 * j] = (T)fp32_value(rnd<T>(xe * cj) - rnd<T>(xo * sj));
+    out.e[2 * j + 1] = (T)fp32_value(rnd<T>(xe * sj) + rnd<T>(xo * cj));
   }
   st<T, V>(dst, out);
 }
@@ -223,9 +223,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(SiluArgs a) {
   Pack<T, V> o;
 #pragma unroll
   for (int e = 0; e < V; ++e) {
-    const float gf = (float)g.e[e];
-    const float sig = 1.f / (1.f + expf(-gf));
-    o.e[e] = (T)(gf * sig * (float)u.e[e]);
+    o.e[e] = (T)swiglu_gate((float)g.e[e], (float)u.e[e]);
   }
   st<T, V>(static_cast<T*>(a.out) + r * a.cols + c, o);
 }

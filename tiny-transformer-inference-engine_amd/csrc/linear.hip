@@ -1,0 +1,325 @@
+// Projections of a decode step, y = x W^T (+ bias), for few rows (tokens):
+// bf16/fp16 storage, fp32 accumulation on MFMA 16x16x32, with the element-
+// wise op that follows the projection in a decoder block fused into the
+// epilogue:
+//   plain   y rounded to the storage type            (nn.Linear)
+//   swiglu  W = [gate rows; up rows]: out = g * sigmoid(g) * u of the rounded
+//           gate / up outputs, rounded once  (kernels/fused_swiglu/kernel.py:6-19)
+//   rope    W = [q rows; k rows; v rows] (MQA_Paged's three projections):
+//           q and k rotated at positions[m], written contiguous, v copied
+//           (models/rope.py:21-47 on serving/paged_mqa.py:76-85's outputs);
+//           the rotation rounds exactly as the stand-alone RoPE kernel does.
+//
+// With tokens in the tens to hundreds, a decode projection is a stream of
+// the weight matrix, and the library GEMMs' large output tiles leave most of
+// the chip idle with long K loops. Here a workgroup owns 16 output features
+// x 16*MB rows and splits K over its 16 wavefronts (each a contiguous K
+// range, so one wavefront reads 64-byte-or-longer runs of each weight row);
+// the wavefronts' fp32 partials are summed through LDS in a fixed order, so
+// results are deterministic and the same in every epilogue. The m tiles of
+// one feature tile are dispatched to one XCD (block ids congruent mod 8), so
+// their common weight rows are fetched from HBM once, into that XCD's L2.
+#include "mfma_decode_common.h"
+
+namespace pkv {
+namespace {
+
+using namespace mfma;
+
+constexpr int kLW = 16;            // wavefronts per workgroup (K split)
+constexpr int kLThreads = 64 * kLW;
+constexpr int kNT = 16;            // output features per tile
+constexpr int kPitch = kNT + 1;    // LDS row pitch of the partial sums (floats)
+
+enum { kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2 };
+
+struct LinArgs {
+  void* out;          // plain / swiglu: [m, n] contiguous
+  const void* x;      // [m, k], rows x_stride elements apart
+  const void* w;      // [rows, k] contiguous (swiglu: 2n rows, gate then up)
+  const void* bias;   // nullable, one per weight row
+  int64_t x_stride;
+  int m;
+  int n;              // output features (swiglu: per half)
+  int k;
+  int m_tiles;
+  int n_tiles;
+  // rope epilogue
+  void* q_out;
+  void* k_out;
+  void* v_out;
+  const int32_t* positions;
+  const float* cos;
+  const float* sin;
+  int max_pos;
+  int hq;
+  int hkv;
+  int d;
+  int* status;
+};
+
+template <typename T>
+__device__ __forceinline__ float rnd(float x) {
+  return (float)(T)fp32_value(x);
+}
+
+template <typename T, int MB, int EPI>
+__global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
+#pragma clang fp contract(off)
+  using v8 = typename Ops<T>::v8;
+  constexpr int MT = 16 * MB;
+  constexpr int NS = EPI == kEpiSwiglu ? 2 : 1;  // weight row sets (gate, up)
+  __shared__ float red[NS][kLW][MT][kPitch];
+
+  const int b = blockIdx.x;
+  const int xcd = b & 7;
+  const int r = b >> 3;
+  const int mt = r % a.m_tiles;
+  const int nt = (r / a.m_tiles) * 8 + xcd;
+  if (nt >= a.n_tiles) return;  // padding tile: the whole workgroup leaves
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int l16 = lane & 15;
+  const int n0 = nt * kNT;
+  const int m0 = mt * MT;
+
+  // operand rows (clamped into range; their outputs are never stored)
+  const T* wrow[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    wrow[s] = static_cast<const T*>(a.w) +
+              (int64_t)(min(n0 + l16, a.n - 1) + s * a.n) * a.k + (lane >> 4) * 8;
+  const T* xrow[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+    xrow[mb] = static_cast<const T*>(a.x) + (int64_t)min(m0 + 16 * mb + l16, a.m - 1) * a.x_stride +
+               (lane >> 4) * 8;
+
+  // this wavefront's contiguous range of 32-wide K steps
+  const int ksteps = a.k >> 5;
+  const int per = (ksteps + kLW - 1) / kLW;
+  const int s0 = w * per;
+  const int s1 = min(s0 + per, ksteps);
+
+  floatx4 acc[NS][MB];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[s][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  v8 av[NS], bv[MB];
+  auto load = [&](int st, v8* A, v8* B) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) A[s] = *reinterpret_cast<const v8*>(wrow[s] + st * 32);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) B[mb] = *reinterpret_cast<const v8*>(xrow[mb] + st * 32);
+  };
+  if (s0 < s1) load(s0, av, bv);
+  for (int st = s0; st < s1; ++st) {
+    v8 an[NS], bn[MB];
+    if (st + 1 < s1) load(st + 1, an, bn);
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[s][mb] = Ops<T>::mma(av[s], bv[mb], acc[s][mb]);
+    if (st + 1 < s1) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) av[s] = an[s];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) bv[mb] = bn[mb];
+    }
+  }
+
+  // lane holds rows m0 + 16 mb + l16, features n0 + 4 (lane >> 4) + i
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[s][w][16 * mb + l16][(lane >> 4) * 4 + i] = acc[s][mb][i];
+  __syncthreads();
+
+  // epilogue: one thread per (row, feature pair)
+  const int t = threadIdx.x;
+  if (t >= MT * (kNT / 2)) return;
+  const int ml = t >> 3;
+  const int p = t & 7;
+  const int m = m0 + ml;
+  const int n = n0 + 2 * p;
+  if (m >= a.m || n >= a.n) return;
+  const bool two = n + 1 < a.n;
+  float v[NS][2];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float sum = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kLW; ++ww) sum += red[s][ww][ml][2 * p + j];
+      v[s][j] = sum;
+    }
+  if (a.bias) {
+    const T* bias = static_cast<const T*>(a.bias);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      v[s][0] = fp32_value(v[s][0] + (float)bias[s * a.n + n]);
+      if (two) v[s][1] = fp32_value(v[s][1] + (float)bias[s * a.n + n + 1]);
+    }
+  }
+
+  if constexpr (EPI == kEpiPlain) {
+    T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
+    o[0] = (T)v[0][0];
+    if (two) o[1] = (T)v[0][1];
+  } else if constexpr (EPI == kEpiSwiglu) {
+    T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (j == 1 && !two) break;
+      o[j] = (T)swiglu_gate(rnd<T>(v[0][j]), rnd<T>(v[1][j]));
+    }
+  } else {
+    // n is even and every region ([q | k | v], d even) starts at an even
+    // feature, so the pair (n, n + 1) is one rotation pair of one head
+    const float xe = rnd<T>(v[0][0]);
+    const float xo = rnd<T>(v[0][1]);
+    const int qn = a.hq * a.d;
+    const int kn = a.hkv * a.d;
+    if (n >= qn + kn) {
+      T* o = static_cast<T*>(a.v_out) + (int64_t)m * kn + (n - qn - kn);
+      o[0] = (T)xe;
+      o[1] = (T)xo;
+      return;
+    }
+    int pos = a.positions[m];
+    if ((unsigned)pos >= (unsigned)a.max_pos) {
+      if (a.status && n == 0) atomicOr(a.status, PKV_STATUS_BAD_POS);
+      pos = 0;
+    }
+    const bool isq = n < qn;
+    const int c = (isq ? n : n - qn) % a.d;
+    const int64_t tix = (int64_t)pos * (a.d >> 1) + (c >> 1);
+    const float cj = rnd<T>(a.cos[tix]);
+    const float sj = rnd<T>(a.sin[tix]);
+    T* o = isq ? static_cast<T*>(a.q_out) + (int64_t)m * qn + n
+               : static_cast<T*>(a.k_out) + (int64_t)m * kn + (n - qn);
+    o[0] = (T)fp32_value(rnd<T>(xe * cj) - rnd<T>(xo * sj));
+    o[1] = (T)fp32_value(rnd<T>(xe * sj) + rnd<T>(xo * cj));
+  }
+}
+
+template <typename T, int EPI>
+int launch_t(LinArgs a, hipStream_t stream) {
+  const int mb = a.m <= 16 ? 1 : 2;
+  a.m_tiles = (a.m + 16 * mb - 1) / (16 * mb);
+  a.n_tiles = (a.n + kNT - 1) / kNT;
+  const int64_t blocks = (int64_t)((a.n_tiles + 7) / 8) * 8 * a.m_tiles;
+  if (blocks > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "linear: %lld tiles", (long long)blocks);
+  if (mb == 1)
+    hipLaunchKernelGGL((linear_kernel<T, 1, EPI>), dim3((unsigned)blocks), dim3(kLThreads), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((linear_kernel<T, 2, EPI>), dim3((unsigned)blocks), dim3(kLThreads), 0,
+                       stream, a);
+  return check_launch("linear_kernel");
+}
+
+template <int EPI>
+int dispatch(const LinArgs& a, int dtype, hipStream_t stream) {
+  if (dtype == PKV_DTYPE_BF16) return launch_t<bf16, EPI>(a, stream);
+  if (dtype == PKV_DTYPE_F16) return launch_t<f16, EPI>(a, stream);
+  return fail(PKV_ERR_UNSUPPORTED, "linear: dtype %d (bf16 / fp16 only)", dtype);
+}
+
+int check_common(const void* out, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                 int64_t x_stride, int dtype) {
+  if (dtype != PKV_DTYPE_BF16 && dtype != PKV_DTYPE_F16)
+    return fail(PKV_ERR_UNSUPPORTED, "linear: dtype %d (bf16 / fp16 only)", dtype);
+  if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x3fffffff || k > 0x7fffffff)
+    return fail(PKV_ERR_INVALID, "linear: bad sizes m=%lld n=%lld k=%lld", (long long)m,
+                (long long)n, (long long)k);
+  if (!out || !x || !w) return fail(PKV_ERR_INVALID, "linear: null pointer argument");
+  if (k % 32 != 0 || x_stride % 8 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)w & 15))
+    return fail(PKV_ERR_UNSUPPORTED,
+                "linear: k (%lld) must be a multiple of 32, x rows 16-byte aligned",
+                (long long)k);
+  if (x_stride < k) return fail(PKV_ERR_INVALID, "linear: x_stride below k");
+  return PKV_OK;
+}
+
+}  // namespace
+}  // namespace pkv
+
+using namespace pkv;
+
+extern "C" {
+
+int pkv_linear(void* out, const void* x, const void* w, const void* bias, int64_t m, int64_t n,
+               int64_t k, int64_t x_stride, int dtype, void* stream) {
+  const int rc = check_common(out, x, w, m, n, k, x_stride, dtype);
+  if (rc != PKV_OK || m == 0) return rc;
+  LinArgs a{};
+  a.out = out;
+  a.x = x;
+  a.w = w;
+  a.bias = bias;
+  a.x_stride = x_stride;
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
+  return dispatch<kEpiPlain>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+int pkv_linear_swiglu(void* out, const void* x, const void* w_gate_up, const void* bias,
+                      int64_t m, int64_t n, int64_t k, int64_t x_stride, int dtype,
+                      void* stream) {
+  const int rc = check_common(out, x, w_gate_up, m, n, k, x_stride, dtype);
+  if (rc != PKV_OK || m == 0) return rc;
+  LinArgs a{};
+  a.out = out;
+  a.x = x;
+  a.w = w_gate_up;
+  a.bias = bias;
+  a.x_stride = x_stride;
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
+  return dispatch<kEpiSwiglu>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+int pkv_linear_rope_qkv(void* q_out, void* k_out, void* v_out, const void* x, const void* w_qkv,
+                        const void* bias, int64_t m, int64_t k, int64_t x_stride,
+                        const int32_t* positions, const float* cos_table,
+                        const float* sin_table, int max_pos, int hq, int hkv, int d, int dtype,
+                        int* status, void* stream) {
+  if (hq <= 0 || hkv <= 0 || d <= 0 || (d & 1) || max_pos <= 0)
+    return fail(PKV_ERR_INVALID, "linear_rope_qkv: bad sizes hq=%d hkv=%d d=%d max_pos=%d", hq,
+                hkv, d, max_pos);
+  const int64_t n = (int64_t)(hq + 2 * hkv) * d;
+  const int rc = check_common(q_out, x, w_qkv, m, n, k, x_stride, dtype);
+  if (rc != PKV_OK) return rc;
+  if (!k_out || !v_out || !positions || !cos_table || !sin_table)
+    return fail(PKV_ERR_INVALID, "linear_rope_qkv: null pointer argument");
+  if (m == 0) return PKV_OK;
+  LinArgs a{};
+  a.x = x;
+  a.w = w_qkv;
+  a.bias = bias;
+  a.x_stride = x_stride;
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.v_out = v_out;
+  a.positions = positions;
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.max_pos = max_pos;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.d = d;
+  a.status = status;
+  return dispatch<kEpiRope>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

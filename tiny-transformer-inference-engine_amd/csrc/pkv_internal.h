@@ -23,6 +23,26 @@ inline int elem_bytes(int dtype) {
   return dtype == PKV_DTYPE_F32 ? 4 : 2;
 }
 
+// x as an fp32 register value the compiler must produce before using it.
+// Without it the backend may fold an fp32 operation and the conversion to
+// fp16 that follows into one mixed-precision instruction (v_fma_mix*) that
+// rounds once, where the framework's element-wise ops round to fp32 and then
+// to fp16; the two differ in rare near-tie cases.
+__device__ __forceinline__ float fp32_value(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// SwiGLU gate of (already rounded) gate / up values, g * sigmoid(g) * u in
+// fp32, the arithmetic of kernels/fused_swiglu/kernel.py:17-18. Contraction
+// is off so that every kernel evaluating it (the stand-alone gate and the
+// projection epilogue) gives the same bits.
+__device__ __forceinline__ float swiglu_gate(float g, float u) {
+#pragma clang fp contract(off)
+  const float sig = 1.f / (1.f + expf(-g));
+  return fp32_value(g * sig * u);
+}
+
 // ---------------------------------------------------------------------------
 // Append / gather (append.hip)
 // ---------------------------------------------------------------------------

@@ -64,6 +64,13 @@ _SIGNATURES = {
                  _c_int),
     "pkv_silu_mul": ([_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp],
                      _c_int),
+    "pkv_linear": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+                    _c_vp], _c_int),
+    "pkv_linear_swiglu": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+                           _c_vp], _c_int),
+    "pkv_linear_rope_qkv": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                             _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                             _c_vp, _c_vp], _c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -11,6 +11,7 @@ captured in a HIP graph.
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
 from . import _native
 
@@ -147,6 +148,99 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
                                     _native.stream_ptr(gate.device))
     _native.check(rc, "silu_mul")
     return out
+
+
+# the few-row projection kernels (csrc/linear.hip) take decode-sized row
+# counts; wider problems (prefill chunks, the vocabulary projection) and
+# fp32 go to the library GEMM
+LINEAR_MAX_ROWS = 256
+LINEAR_MAX_FEATURES = 16384
+
+
+def _as_rows(x: torch.Tensor) -> torch.Tensor:
+    x2 = x.reshape(-1, x.shape[-1]) if x.dim() != 2 else x
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2
+
+
+def _linear_ok(x2: torch.Tensor, w: torch.Tensor, bias, n_features: int) -> bool:
+    return (x2.is_cuda and x2.dtype in (torch.bfloat16, torch.float16) and w.dtype == x2.dtype
+            and (bias is None or (bias.dtype == x2.dtype and bias.is_contiguous()))
+            and 0 < x2.shape[0] <= LINEAR_MAX_ROWS and x2.shape[1] % 32 == 0
+            and n_features <= LINEAR_MAX_FEATURES and w.is_contiguous()
+            and (x2.shape[0] == 1 or x2.stride(0) % 8 == 0)
+            and x2.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+
+
+def _x_stride(x2):
+    return x2.stride(0) if x2.shape[0] > 1 else x2.shape[1]
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None):
+    """x W^T + b. Few-row bf16/fp16 problems run on the split-K MFMA kernel
+    (pkv_linear); others on the library GEMM (F.linear)."""
+    x2 = _as_rows(x)
+    n = weight.shape[0]
+    if not _linear_ok(x2, weight, bias, n):
+        return F.linear(x, weight, bias)
+    out = torch.empty((x2.shape[0], n), dtype=x.dtype, device=x.device)
+    rc = _native.lib().pkv_linear(out.data_ptr(), x2.data_ptr(), weight.data_ptr(),
+                                  _native.ptr(bias), x2.shape[0], n, x2.shape[1], _x_stride(x2),
+                                  _native.dtype_code(x.dtype), _native.stream_ptr(x.device))
+    _native.check(rc, "linear")
+    return out.view(*x.shape[:-1], n)
+
+
+def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor, b_gate_up: torch.Tensor | None):
+    """silu(x Wg^T + bg) * (x Wu^T + bu) with W = [Wg; Wu] (models/mlp.py:24-30
+    with the reference's fused_swiglu arithmetic)."""
+    x2 = _as_rows(x)
+    h = w_gate_up.shape[0] // 2
+    if not _linear_ok(x2, w_gate_up, b_gate_up, 2 * h):
+        gu = F.linear(x, w_gate_up, b_gate_up)
+        return silu_mul(gu[..., :h], gu[..., h:])
+    _native.require_device(x2, w_gate_up, what="linear_swiglu")
+    out = torch.empty((x2.shape[0], h), dtype=x.dtype, device=x.device)
+    rc = _native.lib().pkv_linear_swiglu(
+        out.data_ptr(), x2.data_ptr(), w_gate_up.data_ptr(), _native.ptr(b_gate_up),
+        x2.shape[0], h, x2.shape[1], _x_stride(x2), _native.dtype_code(x.dtype),
+        _native.stream_ptr(x.device))
+    _native.check(rc, "linear_swiglu")
+    return out.view(*x.shape[:-1], h)
+
+
+def linear_rope_qkv(x: torch.Tensor, w_qkv: torch.Tensor, b_qkv: torch.Tensor | None,
+                    positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, hq: int,
+                    hkv: int, d: int):
+    """q, k, v projections of x [T, d_model] with W = [Wq; Wk; Wv], q and k
+    rotated at positions (fp32 tables cos / sin [max_pos, d/2]): contiguous
+    q [T, hq, d], k [T, hkv, d], v [T, hkv, d] (serving/paged_mqa.py:76-85)."""
+    x2 = _as_rows(x)
+    T = x2.shape[0]
+    nq, nk = hq * d, hkv * d
+    if not _linear_ok(x2, w_qkv, b_qkv, nq + 2 * nk):
+        qkv = F.linear(x2, w_qkv, b_qkv)
+        return rope(qkv[:, :nq], qkv[:, nq:nq + nk], positions, cos, sin, v=qkv[:, nq + nk:],
+                    hq=hq, hkv=hkv, d=d)
+    _native.require_device(x2, w_qkv, positions, cos, sin, what="linear_rope_qkv")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError("linear_rope_qkv: cos / sin must be fp32 tables")
+    cos2, sin2 = cos.reshape(-1, d // 2).contiguous(), sin.reshape(-1, d // 2).contiguous()
+    pos = positions if positions.dtype == torch.int32 else positions.to(torch.int32)
+    pos = pos.contiguous()
+    if pos.numel() != T:
+        raise ValueError("linear_rope_qkv: positions and x disagree on the token count")
+    q = torch.empty((T, hq, d), dtype=x.dtype, device=x.device)
+    k = torch.empty((T, hkv, d), dtype=x.dtype, device=x.device)
+    v = torch.empty((T, hkv, d), dtype=x.dtype, device=x.device)
+    rc = _native.lib().pkv_linear_rope_qkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), x2.data_ptr(), w_qkv.data_ptr(),
+        _native.ptr(b_qkv), T, x2.shape[1], _x_stride(x2), pos.data_ptr(), cos2.data_ptr(),
+        sin2.data_ptr(), cos2.shape[0], hq, hkv, d, _native.dtype_code(x.dtype), None,
+        _native.stream_ptr(x.device))
+    _native.check(rc, "linear_rope_qkv")
+    return q, k, v
 
 
 class FusedRows:

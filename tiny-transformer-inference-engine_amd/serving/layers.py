@@ -9,8 +9,8 @@ arithmetic so that state dicts load unchanged and results match:
   ModelConfig     models/model_config.py:8-41
 As in the reference, which routes CUDA tensors to its own kernels
 (models/rmsnorm.py:18, models/mlp.py:30), tensors on a ROCm device go to the
-HIP kernels of fused_ops (RMSNorm, token-major RoPE, the SwiGLU gate, with
-gate and up computed by one GEMM); CPU tensors use the PyTorch formulas.
+HIP kernels of fused_ops (RMSNorm, token-major RoPE, the SwiGLU projections
+with the gate in their epilogue); CPU tensors use the PyTorch formulas.
 """
 from __future__ import annotations
 
@@ -117,9 +117,8 @@ class SwiGLU(nn.Module):
     def forward(self, x):
         if x.is_cuda:
             w, b = self._gate_up.get()
-            gu = F.linear(x, w, b)
-            h = self.gate_proj.out_features
-            return self.down_proj(fused_ops.silu_mul(gu[..., :h], gu[..., h:]))
+            h = fused_ops.linear_swiglu(x, w, b)
+            return fused_ops.linear(h, self.down_proj.weight, self.down_proj.bias)
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 

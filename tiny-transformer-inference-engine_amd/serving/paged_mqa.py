@@ -8,8 +8,8 @@ same two entry points:
   forward_paged(x [1, SQ, d_model], pool, layer_idx, block_table, start)
   forward_paged_batched(x [T, d_model], pool, layer_idx, positions,
                         query_start_loc, block_tables)
-The step runs: one GEMM for the q/k/v projections, RoPE as one HIP kernel,
-the slot-mapped K/V append and the paged attention as HIP kernels
+The step runs: the q/k/v projections and RoPE as one HIP kernel, the
+slot-mapped K/V append and the paged attention as HIP kernels
 (libpagedkv.so), then the output projection. The per-sequence slot-mapping loop of the reference
 (paged_mqa.py:87-99) becomes one in-kernel slot computation from
 device-resident block tables.
@@ -18,9 +18,9 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from .fake_paged_attn import paged_attention_append_meta, paged_attention_meta
+from . import fused_ops
 from .fused_ops import FusedRows
 from .layers import RoPE
 from .paged_meta import PagedBatchMeta, pack_batch_meta
@@ -91,17 +91,13 @@ class MQA_Paged(nn.Module):
     def forward_meta(self, x, pool, layer_idx, meta: PagedBatchMeta):
         """One layer of a step whose metadata is already on the device."""
         T, d_model = x.shape
-        # q, k, v by one GEMM over the row-concatenated projection weights;
-        # the RoPE kernel reads the three column ranges in place and writes
-        # contiguous rotated q, k (and v)
+        # q, k, v by one projection over the row-concatenated weights with
+        # RoPE in its epilogue (contiguous rotated q, k and v)
         w, b = self._qkv.get()
-        qkv = F.linear(x, w, b)
-        nq, nk = self.num_heads * self.headdim, self.num_kv_heads * self.headdim
-        q = qkv[:, :nq].view(T, self.num_heads, self.headdim)
-        k = qkv[:, nq:nq + nk].view(T, self.num_kv_heads, self.headdim)
-        v = qkv[:, nq + nk:].view(T, self.num_kv_heads, self.headdim)
-        q, k, v = self.rope.forward_tokens(q, k, meta.positions, v=v)
+        cos, sin = self.rope._tables_fp32()
+        q, k, v = fused_ops.linear_rope_qkv(x, w, b, meta.positions, cos, sin, self.num_heads,
+                                            self.num_kv_heads, self.headdim)
 
         # append + attention in one library call (fused on the decode kernels)
-        out = paged_attention_append_meta(q.contiguous(), k, v, pool, layer_idx, meta)
-        return self.out(out.view(T, d_model))
+        out = paged_attention_append_meta(q, k, v, pool, layer_idx, meta)
+        return fused_ops.linear(out.view(T, d_model), self.out.weight, self.out.bias)
