@@ -160,6 +160,7 @@ def run_model(args, torch):
     from serving.kv_pool import KVPool
     from serving.layers import ModelConfig
     from serving.paged_meta import pack_batch_meta
+    from serving import fused_ops
     from serving.paged_model import PagedTransformer
 
     dev = torch.device("cuda:0")
@@ -184,7 +185,7 @@ def run_model(args, torch):
     def step():
         nonlocal ids
         logits = model.forward_step(ids, pool, meta)
-        ids = logits.argmax(-1)
+        ids = fused_ops.argmax_rows(logits)
         # advance every sequence by one token, on the device
         meta.positions.add_(1)
         meta.start_pos.add_(1)

@@ -45,6 +45,9 @@
  *   pkv_linear_swiglu     gate_proj, up_proj and fused_swiglu
  *                                                    models/mlp.py:24-30
  *   pkv_linear_rope_qkv   q/k/v projections and RoPE serving/paged_mqa.py:76-85
+ *   pkv_argmax_rows       greedy token choice: logits.argmax per sequence
+ *                                                    serving/generation.py:77,88,132,142;
+ *                         greedy()                   sampling.py:5-137
  */
 #ifndef PAGEDKV_H
 #define PAGEDKV_H
@@ -294,6 +297,18 @@ int pkv_linear_rope_qkv(void* q_out, void* k_out, void* v_out, const void* x, co
                         const int32_t* positions, const float* cos_table,
                         const float* sin_table, int max_pos, int hq, int hkv, int d, int dtype,
                         int* status, void* stream);
+
+/*
+ * Greedy token choice: ids[r] (int64) = the index of the largest of the
+ * `vocab` logits of row r (rows row_stride elements apart, dtype F32 / F16 /
+ * BF16). Same result as the framework's argmax: the first index holding the
+ * maximum, and a NaN counts as larger than any number (the first NaN
+ * wins). Replaces logits.argmax as taken per sequence by the greedy loops
+ * (serving/generation.py:77, :88, :132, :142) and greedy()
+ * (sampling.py:5-137).
+ */
+int pkv_argmax_rows(int64_t* ids, const void* logits, int64_t rows, int64_t vocab,
+                    int64_t row_stride, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@
 // With tokens in the tens to hundreds, a decode projection is a stream of
 // the weight matrix, and the library GEMMs' large output tiles leave most of
 // the chip idle with long K loops. Here a workgroup owns 16 output features
-// x 16*MB rows and splits K over its 16 wavefronts (each a contiguous K
+// x 16*MB rows and splits K over its 8 wavefronts (each a contiguous K
 // range, so one wavefront reads 64-byte-or-longer runs of each weight row);
 // the wavefronts' fp32 partials are summed through LDS in a fixed order, so
 // results are deterministic and the same in every epilogue. The m tiles of
@@ -26,7 +26,7 @@ namespace {
 
 using namespace mfma;
 
-constexpr int kLW = 16;            // wavefronts per workgroup (K split)
+constexpr int kLW = 8;             // wavefronts per workgroup (K split)
 constexpr int kLThreads = 64 * kLW;
 constexpr int kNT = 16;            // output features per tile
 constexpr int kPitch = kNT + 1;    // LDS row pitch of the partial sums (floats)
@@ -95,6 +95,24 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
     xrow[mb] = static_cast<const T*>(a.x) + (int64_t)min(m0 + 16 * mb + l16, a.m - 1) * a.x_stride +
                (lane >> 4) * 8;
 
+  // epilogue mapping: one thread per (row, feature pair)
+  const int t = threadIdx.x;
+  const int ml = t >> 3;
+  const int p = t & 7;
+  const int m = m0 + ml;
+  const int n = n0 + 2 * p;
+  const bool live = t < MT * (kNT / 2) && m < a.m && n < a.n;
+  // rope: the row's position is requested before the operands and its
+  // table entries right after them, so neither dependent load is waited
+  // for after the reduction
+  const int qn = a.hq * a.d;
+  const int kn = a.hkv * a.d;
+  const bool rot = EPI == kEpiRope && live && n < qn + kn;
+  int pos = 0;
+  if constexpr (EPI == kEpiRope) {
+    if (rot) pos = a.positions[m];
+  }
+
   // this wavefront's contiguous range of 32-wide K steps
   const int ksteps = a.k >> 5;
   const int per = (ksteps + kLW - 1) / kLW;
@@ -114,6 +132,22 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
     for (int mb = 0; mb < MB; ++mb) B[mb] = *reinterpret_cast<const v8*>(xrow[mb] + st * 32);
   };
   if (s0 < s1) load(s0, av, bv);
+  float cj = 0.f, sj = 0.f;
+  bool bad_pos = false;
+  if constexpr (EPI == kEpiRope) {
+    if (rot) {
+      if ((unsigned)pos >= (unsigned)a.max_pos) {
+        // the framework gather would fault on this index; flag it and
+        // rotate by angle 0 instead of reading outside the tables
+        bad_pos = true;
+        pos = 0;
+      }
+      const int c = (n < qn ? n : n - qn) % a.d;
+      const int64_t tix = (int64_t)pos * (a.d >> 1) + (c >> 1);
+      cj = a.cos[tix];
+      sj = a.sin[tix];
+    }
+  }
   for (int st = s0; st < s1; ++st) {
     v8 an[NS], bn[MB];
     if (st + 1 < s1) load(st + 1, an, bn);
@@ -138,14 +172,7 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
       for (int i = 0; i < 4; ++i) red[s][w][16 * mb + l16][(lane >> 4) * 4 + i] = acc[s][mb][i];
   __syncthreads();
 
-  // epilogue: one thread per (row, feature pair)
-  const int t = threadIdx.x;
-  if (t >= MT * (kNT / 2)) return;
-  const int ml = t >> 3;
-  const int p = t & 7;
-  const int m = m0 + ml;
-  const int n = n0 + 2 * p;
-  if (m >= a.m || n >= a.n) return;
+  if (!live) return;
   const bool two = n + 1 < a.n;
   float v[NS][2];
 #pragma unroll
@@ -182,24 +209,16 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
     // feature, so the pair (n, n + 1) is one rotation pair of one head
     const float xe = rnd<T>(v[0][0]);
     const float xo = rnd<T>(v[0][1]);
-    const int qn = a.hq * a.d;
-    const int kn = a.hkv * a.d;
-    if (n >= qn + kn) {
+    if (!rot) {
       T* o = static_cast<T*>(a.v_out) + (int64_t)m * kn + (n - qn - kn);
       o[0] = (T)xe;
       o[1] = (T)xo;
       return;
     }
-    int pos = a.positions[m];
-    if ((unsigned)pos >= (unsigned)a.max_pos) {
-      if (a.status && n == 0) atomicOr(a.status, PKV_STATUS_BAD_POS);
-      pos = 0;
-    }
+    if (bad_pos && a.status && n == 0) atomicOr(a.status, PKV_STATUS_BAD_POS);
+    cj = rnd<T>(cj);
+    sj = rnd<T>(sj);
     const bool isq = n < qn;
-    const int c = (isq ? n : n - qn) % a.d;
-    const int64_t tix = (int64_t)pos * (a.d >> 1) + (c >> 1);
-    const float cj = rnd<T>(a.cos[tix]);
-    const float sj = rnd<T>(a.sin[tix]);
     T* o = isq ? static_cast<T*>(a.q_out) + (int64_t)m * qn + n
                : static_cast<T*>(a.k_out) + (int64_t)m * kn + (n - qn);
     o[0] = (T)fp32_value(rnd<T>(xe * cj) - rnd<T>(xo * sj));

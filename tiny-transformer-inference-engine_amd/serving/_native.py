@@ -71,6 +71,7 @@ _SIGNATURES = {
     "pkv_linear_rope_qkv": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                              _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                              _c_vp, _c_vp], _c_int),
+    "pkv_argmax_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp], _c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -1,10 +1,13 @@
-"""Host wrappers of the decoder block's element-wise kernels in libpagedkv.so
-(csrc/layers.hip): RMSNorm with a fused residual add, RoPE on token-major
-Q/K rows (optionally split out of one fused projection output), and the
-SwiGLU gate.
+"""Host wrappers of the decoder block's kernels around the paged attention in
+libpagedkv.so: RMSNorm with a fused residual add, RoPE on token-major Q/K
+rows, and the SwiGLU gate (csrc/layers.hip); the few-row projections with
+those ops fused into their epilogues (csrc/linear.hip); the greedy argmax
+(csrc/sampling.hip).
 
-Every function requires ROCm device tensors and the library; there is no
-framework fallback (RuntimeError otherwise). Outputs are allocated with
+Every function requires ROCm device tensors and the library (RuntimeError
+otherwise). The projections hand shapes their kernel does not take (fp32,
+k not a multiple of 32, more than LINEAR_MAX_ROWS rows or LINEAR_MAX_FEATURES
+features) to the library GEMM. Outputs are allocated with
 torch on the input's device and the current stream, so the calls can be
 captured in a HIP graph.
 """
@@ -241,6 +244,29 @@ def linear_rope_qkv(x: torch.Tensor, w_qkv: torch.Tensor, b_qkv: torch.Tensor | 
         _native.stream_ptr(x.device))
     _native.check(rc, "linear_rope_qkv")
     return q, k, v
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Index of the largest logit of every row of [rows, vocab] logits as
+    int64 [rows] (pkv_argmax_rows; the framework's argmax result: first
+    maximum, NaN above every number). With `out`, the ids are written there
+    (an int64 device tensor of rows elements)."""
+    _native.require_device(logits, what="argmax_rows")
+    if logits.dim() != 2:
+        raise ValueError(f"argmax_rows: expected [rows, vocab], got {tuple(logits.shape)}")
+    lg = logits if logits.stride(1) == 1 else logits.contiguous()
+    rows, vocab = lg.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.long, device=logits.device)
+    elif (out.dtype != torch.long or out.numel() != rows or not out.is_contiguous()
+          or out.device != logits.device):
+        raise ValueError("argmax_rows: out must be a contiguous int64 tensor of rows elements")
+    stride = lg.stride(0) if rows > 1 else vocab
+    rc = _native.lib().pkv_argmax_rows(out.data_ptr(), lg.data_ptr(), rows, vocab, stride,
+                                       _native.dtype_code(lg.dtype),
+                                       _native.stream_ptr(logits.device))
+    _native.check(rc, "argmax_rows")
+    return out
 
 
 class FusedRows:

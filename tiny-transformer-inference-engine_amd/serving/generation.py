@@ -13,13 +13,13 @@ from __future__ import annotations
 import torch
 
 from .batch import build_batch_step
-from .sampling import sample
+from .sampling import greedy, sample
 from .sequence import Sequence
 
 
 def _argmax_tokens(logits):
-    # one device->host copy per step for the whole batch
-    return logits.argmax(dim=-1).tolist()
+    # one argmax launch and one device->host copy per step for the whole batch
+    return greedy(logits)[:, 0].tolist()
 
 
 @torch.no_grad()

@@ -21,6 +21,8 @@ from __future__ import annotations
 
 import torch
 
+from . import fused_ops
+
 
 class DecodeStepGraph:
     """Greedy decode step over a fixed batch, replayed from a HIP graph.
@@ -57,7 +59,7 @@ class DecodeStepGraph:
 
     def _step(self):
         logits = self.model.forward_step(self.ids, self.pool, self.meta)
-        self.ids.copy_(logits.argmax(-1))
+        fused_ops.argmax_rows(logits, out=self.ids)
         self.meta.positions.add_(1)
         self.meta.start_pos.add_(1)
         self.meta.seq_lens.add_(1)

@@ -12,8 +12,14 @@ import math
 import torch
 import torch.nn.functional as F
 
+from . import fused_ops
+
 
 def greedy(logits):
+    """[batch, vocab] -> [batch, 1] argmax; on a ROCm device one HIP kernel
+    (fused_ops.argmax_rows, same ties and NaN order as torch.argmax)."""
+    if logits.is_cuda and logits.dim() == 2 and logits.shape[-1] > 0:
+        return fused_ops.argmax_rows(logits)[:, None]
     return torch.argmax(logits, dim=-1, keepdim=True)
 
 
