@@ -14,7 +14,7 @@ with the gate in their epilogue); CPU tensors use the PyTorch formulas.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 import torch.nn as nn
@@ -159,3 +159,25 @@ class ModelConfig:
     def hidden_size(self) -> int:
         # the reference's MLP width equals d_model (model_config.py:32-34)
         return self.d_model
+
+
+@dataclass
+class SchedulerConfig:
+    """Scheduler limits (reference: models/model_config.py:56-70, where the
+    fields exist but the reference scheduler does not read them; here
+    serving.scheduler.Scheduler honours them when given one).
+    cudagraph_batch_sizes is kept for the API; decode graphs are captured per
+    batch by serving.graph_step.DecodeStepGraph instead."""
+    max_num_seqs: int = 32
+    max_num_batched_tokens: int = 512
+    enable_chunked_prefill: bool = False
+    preemption: str = "recompute"
+    policy: str = "fcfs"
+    cudagraph_batch_sizes: list = field(default_factory=lambda: [1, 2, 4, 8, 16, 32])
+
+    def __post_init__(self):
+        assert self.max_num_batched_tokens >= self.max_num_seqs, \
+            "every decode takes 1 token, so the budget must cover all seqs"
+        assert self.preemption == "recompute"
+        assert self.policy == "fcfs"
+        assert max(self.cudagraph_batch_sizes) <= self.max_num_seqs
