@@ -1,8 +1,8 @@
 """The MFMA prefill / chunked-prefill kernel (csrc/prefill_mfma.hip) against
 the fp64 oracle (bf16 / fp16: 2e-2 absolute, lse too).
 
-Shapes: 16 or 32 query heads per KV head (8 or 4 query tokens per 128-row
-tile), head dim 64 / 128, 1 or 2 KV heads, block size 16 / 32; query runs
+Shapes: 16 or 32 query heads per KV head (8 or 4 query tokens per tile; 8
+with two 16-head row tiles per wavefront for long runs at 32), head dim 64 / 128, 1 or 2 KV heads, block size 16 / 32; query runs
 not a multiple of the tile's tokens, runs longer than the context
 (kv_len < q_len), an empty context, a one-sequence batch (no decode split),
 causal and not, a custom scale.
@@ -44,6 +44,8 @@ CASES = {
     "short_kv": [(40, 20), (16, 0), (50, 50)],
     # a single sequence: no decode split
     "single": [(300, 1300)],
+    # query runs of 256+ tokens over 512+ keys: 8-token tiles at 32 heads per kv head
+    "wide": [(512, 512), (260, 900), (7, 7)],
 }
 
 

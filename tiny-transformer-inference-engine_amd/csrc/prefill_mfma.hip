@@ -7,18 +7,21 @@
 // alignment, :196-207, :315-329); no visible key gives a zero row and
 // lse = +inf (:418-446).
 //
-// A workgroup of 8 wavefronts owns a tile of 128 (query token, head) rows of
-// one KV head - 4 tokens x 32 heads or 8 tokens x 16 heads - and each
-// wavefront 16 of them (16 heads of one token). The tile's keys are walked
+// A workgroup of 8 wavefronts owns a tile of query tokens of one KV head:
+// each token's G heads are covered by WPT wavefronts of NT 16-head row tiles
+// each (G = 16 NT WPT; the NT tiles of a wavefront share every K and V^T
+// fragment it reads), so a tile holds TQ = 8 / WPT tokens: 8 tokens x 16
+// heads, 4 x 32, or 8 x 32 with two row tiles per wavefront, chosen by the
+// host for long contexts (fewer K/V re-reads across tiles). The tile's keys are walked
 // in 32-token chunks staged once in LDS (double-buffered: the next chunk's
 // loads are in flight while the wavefronts compute on the current one) and
-// shared by all 8 wavefronts, so each K/V row is read once per tile for 128
-// rows. Per wavefront and chunk: S^T = K Q^T, online softmax with its
+// shared by all 8 wavefronts, so each K/V row is read once per tile for
+// TQ G rows. Per wavefront and chunk: S^T = K Q^T, online softmax with its
 // token's causal limit, O^T += V^T P^T (the decode kernels' MFMA steps).
 //
 // Grid: one workgroup per tile slot, 1-D. Sequence s owns the slots
 // [base_s, base_s + ceil(q_len_s / TQ)), base_s = query_start_loc[s] / TQ + s
-// (TQ = tokens per tile), a non-decreasing function of s, so
+// (TQ tokens per tile), a non-decreasing function of s, so
 // ceil(T / TQ) + n_seq slots cover every tile and a workgroup finds its
 // sequence with one parallel pass over query_start_loc; slots past a
 // sequence's tiles, and sequences another launch owns (qfilter), exit.
@@ -31,10 +34,9 @@ using namespace mfma;
 
 constexpr int kPW = 8;             // wavefronts per workgroup
 constexpr int kPBlock = 64 * kPW;  // threads
-constexpr int kPRows = 16 * kPW;   // (token, head) rows per tile
 
-template <typename T, int D, bool OFF64>
-__global__ __launch_bounds__(kPBlock, 4) void prefill_mfma_kernel(AttnArgs a) {
+template <typename T, int D, int NT, int WPT, bool OFF64>
+__global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(AttnArgs a) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
   constexpr int DT = D / 16;
@@ -49,8 +51,8 @@ __global__ __launch_bounds__(kPBlock, 4) void prefill_mfma_kernel(AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  const int G = a.group;
-  const int TQ = kPRows / G;
+  constexpr int G = 16 * NT * WPT;
+  constexpr int TQ = kPW / WPT;
   const int kvh = blockIdx.y;
   const int slot = blockIdx.x;
 
@@ -79,18 +81,18 @@ __global__ __launch_bounds__(kPBlock, 4) void prefill_mfma_kernel(AttnArgs a) {
   const int ctx = a.causal ? max(kv_len - q_len, 0) : 0;
   const int i0 = tile * TQ;
   const int ntok = min(TQ, q_len - i0);
-  // this wavefront's rows: 16 heads of token i
-  const int ti = (16 * w) / G;
+  // this wavefront's rows: NT 16-head tiles of token i
+  const int ti = w / WPT;
   const bool active = ti < ntok;
   const int i = i0 + (active ? ti : 0);
-  const int h0 = (16 * w) % G;
+  const int h0 = (w % WPT) * 16 * NT;
   const int lim = !active ? 0 : a.causal ? min(kv_len, ctx + i + 1) : kv_len;
   const int kv_hi = a.causal ? min(kv_len, ctx + i0 + ntok) : kv_len;  // the tile's last token's
 
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const int64_t qrow0 = (int64_t)(q_begin + i) * a.hq + kvh * G + h0;
-  v8 qf[1][D / 32];
-  load_q<T, D, 1>(qf, q, qrow0, lane >> 4, lane & 15);
+  v8 qf[NT][D / 32];
+  load_q<T, D, NT>(qf, q, qrow0, lane >> 4, lane & 15);
 
   const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
   const char* kbase = static_cast<const char*>(a.k_pool);
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(kPBlock, 4) void prefill_mfma_kernel(AttnArgs a) {
   cx.grp = lane >> 4;
   cx.l16 = lane & 15;
   cx.scale_log2 = a.scale_log2;
-  WaveState<1, DT> st;
+  WaveState<NT, DT> st;
   st.reset();
   bool bad_block = false;
 
@@ -172,36 +174,51 @@ __global__ __launch_bounds__(kPBlock, 4) void prefill_mfma_kernel(AttnArgs a) {
       cx.vl = kl + Geo::BYTES;
       cx.seg_lo = lo;
       cx.seg_hi = min(lim, hi);
-      if (lo + c * kChunk < cx.seg_hi) compute_chunk<T, D, 1>(c, cx, qf, st);
+      if (lo + c * kChunk < cx.seg_hi) compute_chunk<T, D, NT>(c, cx, qf, st);
     }
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
 
-  // ---- finalise this wavefront's 16 rows
-  st.l[0] = head_lanes_sum(st.l[0]);
+  // ---- finalise this wavefront's 16 NT rows
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) st.l[nt] = head_lanes_sum(st.l[nt]);
   if (!active) return;
-  const int64_t row = qrow0 + (lane & 15);
-  const float L = st.l[0];
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  T* __restrict__ out = static_cast<T*>(a.out) + row * D + 4 * (lane >> 4);
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int nt = 0; nt < NT; ++nt) {
+    const int64_t row = qrow0 + 16 * nt + (lane & 15);
+    const float L = st.l[nt];
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    T* __restrict__ out = static_cast<T*>(a.out) + row * D + 4 * (lane >> 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) out[16 * dt + e] = (T)(st.o[0][dt][e] * inv);
-  if ((lane >> 4) == 0 && a.lse) a.lse[row] = L > 0.f ? (st.m[0] + log2f(L)) * kLn2f : INFINITY;
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[16 * dt + e] = (T)(st.o[nt][dt][e] * inv);
+    if ((lane >> 4) == 0 && a.lse)
+      a.lse[row] = L > 0.f ? (st.m[nt] + log2f(L)) * kLn2f : INFINITY;
+  }
+}
+
+template <typename T, int NT, int WPT, bool OFF64>
+int launch_nt(const AttnArgs& a, hipStream_t stream) {
+  constexpr int tq = kPW / WPT;
+  const dim3 grid((a.n_tokens + tq - 1) / tq + a.n_seq, a.hkv);
+  if (a.d == 64)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, NT, WPT, OFF64>), grid, dim3(kPBlock), 0,
+                       stream, a);
+  else if (a.d == 128)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, NT, WPT, OFF64>), grid, dim3(kPBlock), 0,
+                       stream, a);
+  else
+    return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: d=%d", a.d);
+  return check_launch("prefill_mfma_kernel");
 }
 
 template <typename T, bool OFF64>
 int launch_t(const AttnArgs& a, hipStream_t stream) {
-  const int tq = kPRows / a.group;
-  const dim3 grid((a.n_tokens + tq - 1) / tq + a.n_seq, a.hkv);
-  if (a.d == 64)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, OFF64>), grid, dim3(kPBlock), 0, stream, a);
-  else if (a.d == 128)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, OFF64>), grid, dim3(kPBlock), 0, stream, a);
-  else
-    return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: d=%d", a.d);
-  return check_launch("prefill_mfma_kernel");
+  if (a.group == 16) return launch_nt<T, 1, 1, OFF64>(a, stream);
+  if (a.group == 32 && a.tile_rows == 256) return launch_nt<T, 2, 1, OFF64>(a, stream);
+  if (a.group == 32) return launch_nt<T, 1, 2, OFF64>(a, stream);
+  return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: %d query heads per kv head", a.group);
 }
 
 }  // namespace
@@ -213,7 +230,8 @@ bool prefill_mfma_supported(int dtype, int group, int d) {
 
 int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t stream) {
   if (!a.qloc) return fail(PKV_ERR_INVALID, "prefill_mfma: query_start_loc required");
-  const int64_t slots = ((int64_t)a.n_tokens + kPRows / a.group - 1) / (kPRows / a.group) + a.n_seq;
+  const int tq = a.group == 32 && a.tile_rows != 256 ? kPW / 2 : kPW;
+  const int64_t slots = ((int64_t)a.n_tokens + tq - 1) / tq + a.n_seq;
   if (slots > 0x7fffffff)
     return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: %lld tile slots", (long long)slots);
   const bool off64 = pool_needs_off64(a);
