@@ -30,6 +30,8 @@ namespace mfma {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
 
 template <typename T>
 struct Ops;
@@ -314,15 +316,22 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
   }
 
   // O^T += V^T P^T; V^T fragment: dims 16dt + l16, the same 8 tokens
+  // (4grp + e and 16 + 4grp + e), read out of the row-major chunk by two
+  // gfx950 transposing LDS reads. ds_read_b64_tr_b16 treats the four
+  // 16-bit values each lane of a 16-lane group addresses as a 16 x 4 matrix
+  // and returns lane 4i + c the values c of source lanes i, 4 + i, 8 + i,
+  // 12 + i; so source lane s addresses token row 4grp + s / 4 (and 16 rows
+  // further for the second read), dims 16dt + 4 (s % 4) ... + 3.
+  const char* vt = cx.vl + (4 * cx.grp + (cx.l16 >> 2)) * Geo::PITCH + 8 * (cx.l16 & 3);
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(vt + 32 * dt));
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(vt + 32 * dt + 16 * Geo::PITCH));
+    const v8s both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     v8 vf;
-    const int d = 16 * dt + cx.l16;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int tok = (e < 4 ? 0 : 16) + 4 * cx.grp + (e & 3);
-      vf[e] = *reinterpret_cast<const T*>(cx.vl + Geo::off(tok, d >> 3) + (d & 7) * 2);
-    }
+    __builtin_memcpy(&vf, &both, 16);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) st.o[nt][dt] = Ops<T>::mma(vf, pf[nt], st.o[nt][dt]);
   }

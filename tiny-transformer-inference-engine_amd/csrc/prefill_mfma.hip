@@ -130,13 +130,15 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
     for (int e = tid; e < nblk; e += kPBlock) tbl[e] = table[blk_lo + e];
     __syncthreads();
     const int nch = (hi - lo + kChunk - 1) / kChunk;
-    u32x4 rg[PER];
-    unsigned okm = 0;
     // chunk c's pieces into registers; rows past hi re-read the window's
     // last row (masked), rows whose table entry is outside the pool read
-    // block 0 and are zeroed when staged. Issued for every c < nch + 1
-    // (the last one re-reads chunk nch - 1) so no load sits under a branch.
-    auto issue = [&](int c) {
+    // block 0 and are zeroed when staged. Two register sets alternate, so
+    // two chunks are in flight while one is computed; issued for every
+    // c < nch + 2 (past the end they re-read chunk nch - 1) so no load sits
+    // under a branch.
+    u32x4 rgA[PER], rgB[PER];
+    unsigned okA = 0, okB = 0;
+    auto issue = [&](int c, u32x4 (&rg)[PER], unsigned& okm) {
       c = min(c, nch - 1);
       okm = 0;
 #pragma unroll
@@ -158,8 +160,10 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
         }
       }
     };
-    issue(0);
-    for (int c = 0; c < nch; ++c) {
+    // stage chunk c into LDS buffer c & 1 (free: every wavefront passed the
+    // previous barrier after computing chunk c - 2), request chunk c + 2
+    // into the same registers, then compute chunk c
+    auto step = [&](int c, u32x4 (&rg)[PER], unsigned& okm) {
       char* kl = buf[c & 1];
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
@@ -168,13 +172,19 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
         *reinterpret_cast<u32x4*>(kl + (is_v(k) ? Geo::BYTES : 0) + Geo::off(prow[k], pcol[k])) =
             ok ? rg[k] : u32x4{0u, 0u, 0u, 0u};
       }
-      issue(c + 1);
+      issue(c + 2, rg, okm);
       __syncthreads();  // chunk c is staged; nobody reads the other buffer any more
       cx.kl = kl;
       cx.vl = kl + Geo::BYTES;
       cx.seg_lo = lo;
       cx.seg_hi = min(lim, hi);
       if (lo + c * kChunk < cx.seg_hi) compute_chunk<T, D, NT>(c, cx, qf, st);
+    };
+    issue(0, rgA, okA);
+    issue(1, rgB, okB);
+    for (int c = 0; c < nch; c += 2) {
+      step(c, rgA, okA);
+      if (c + 1 < nch) step(c + 1, rgB, okB);  // uniform across the workgroup
     }
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
