@@ -65,10 +65,16 @@ extern "C" {
 #define PKV_DTYPE_F16 1
 #define PKV_DTYPE_BF16 2
 
-/* part_tokens value of pkv_paged_attention selecting the persistent
-   (stream-K) decode kernel where it applies (bf16/f16, one query per
-   sequence, 16 or 32 query heads per kv head, d = 64 or 128). */
+/* part_tokens values of pkv_paged_attention selecting a persistent decode
+   kernel where it applies (bf16/f16, one query per sequence, 16 or 32
+   query heads per kv head, d = 64 or 128): PKV_PART_PERSISTENT the one the
+   library prefers (currently the static one), PKV_PART_STATIC the one with
+   static equal shares, PKV_PART_DYNAMIC the dynamically scheduled one (up
+   to 1024 sequence x kv head pairs, block_size >= 16; else the static
+   one). */
 #define PKV_PART_PERSISTENT (-1)
+#define PKV_PART_STATIC (-2)
+#define PKV_PART_DYNAMIC (-3)
 
 #define PKV_OK 0
 #define PKV_ERR_INVALID (-1)     /* bad argument (shape, null pointer, ...) */
@@ -135,8 +141,10 @@ int pkv_gather(void* k_out, void* v_out, const void* k_pool,
 /*
  * Bytes of workspace pkv_paged_attention needs for this problem (0 when no
  * sequence is split). `max_kv_len` <= 0 means max_blk * block_size.
- * The workspace holds partial results between the kernels of one call and
- * needs no initialisation. Calls that overlap on one workspace race.
+ * The workspace holds partial results and, in its first 256 KiB, the
+ * persistent kernel's per-sequence arrival counters: zero-fill it once
+ * before its first use; every call leaves the counters zero again. Calls
+ * that overlap on one workspace race.
  */
 size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
                                      int d, int max_blk, int block_size,
@@ -163,8 +171,10 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
  * capacity) must bound every kv_len; `part_tokens` is the split-K
  * partition length (0: automatic, the persistent kernel for context bounds
  * of 4096 tokens and more where it applies, else fixed partitions;
- * PKV_PART_PERSISTENT: one persistent workgroup per CU slot, each taking an
- * equal share of all context chunks).
+ * PKV_PART_STATIC: persistent workgroups each taking an equal share of all
+ * context chunks; PKV_PART_DYNAMIC: one persistent workgroup per CU drawing
+ * work items (whole sequences, pieces of long ones) largest first;
+ * PKV_PART_PERSISTENT: the persistent kernel the library prefers).
  * Workspace: pkv_attention_workspace_bytes().
  */
 int pkv_paged_attention(void* out, float* lse, const void* q,

@@ -1,6 +1,8 @@
-"""The two MFMA decode kernels (the split-K partition form, the default, and
-the persistent stream-K form selected by part_tokens = PART_PERSISTENT)
-against the fp64 oracle, on the shapes that stress their work decomposition:
+"""The MFMA decode kernels (the split-K partition form, the default; the
+static-share persistent form, part_tokens = PART_STATIC; the dynamically
+scheduled persistent form, PART_DYNAMIC; PART_PERSISTENT, the one the
+library prefers) against the fp64 oracle, on the shapes that stress their
+work decomposition:
 
   - one very long sequence, cut by every workgroup share (all partials,
     one last-arriving merger);
@@ -21,6 +23,8 @@ from serving.fake_paged_attn import paged_attn_fwd, paged_mqa_decode
 
 pytestmark = pytest.mark.gpu
 SK = _native.PART_PERSISTENT
+STATIC = _native.PART_STATIC
+DYN = _native.PART_DYNAMIC
 DEV = "cuda"
 SHAPES = [(16, 64), (32, 128), (16, 128), (32, 64)]  # (heads per kv head, D)
 
@@ -49,7 +53,7 @@ def check(out, lse, eo, el, what):
 
 
 @pytest.mark.parametrize("g,d", SHAPES)
-@pytest.mark.parametrize("part_tokens", [SK, 0, 512])
+@pytest.mark.parametrize("part_tokens", [SK, STATIC, DYN, 0, 512])
 def test_single_long_sequence(g, d, part_tokens):
     print(f"[decode long] g={g} d={d} part={part_tokens}", flush=True)
     p = workloads.decode_problem([30000], g, 1, d, 16, 2048, torch.bfloat16, DEV, seed=11)
@@ -72,12 +76,13 @@ def test_many_short_and_empty_sequences_repeated(g, d):
                                  DEV, seed=12)
     seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
     eo, el = oracle(p, seq_lens)
-    for rep in range(3):
+    for rep in range(4):
+        pt = DYN if rep % 2 == 0 else STATIC
         lse = torch.empty(len(lens), g, device=DEV)
         out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
-                               part_tokens=SK)
+                               part_tokens=pt)
         torch.cuda.synchronize()
-        check(out, lse, eo, el, f"short rep {rep}")
+        check(out, lse, eo, el, f"short rep {rep} part_tokens={pt}")
     # the partition kernel agrees
     out2 = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, part_tokens=256)
     check(out2, None, eo, el, "partition kernel")
@@ -96,7 +101,7 @@ def test_gqa_two_kv_heads_and_missing_queries(dtype):
     eo, el = ref.paged_attention(np64(q), np64(p.k_pool), np64(p.v_pool),
                                  p.block_tables.cpu().numpy(), p.seq_lens.cpu().numpy(),
                                  qsl.cpu().numpy())
-    for pt in (0, SK):
+    for pt in (0, SK, STATIC, DYN):
         O = torch.empty_like(q)
         L = torch.empty(T, g * hkv, device=DEV)
         paged_mqa_decode(q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, out=O, lse=L,
@@ -108,6 +113,8 @@ def test_gqa_two_kv_heads_and_missing_queries(dtype):
 def test_cfg4_and_cfg5_kernels_agree():
     for name, p in [("cfg4", workloads.cfg4_problem(DEV)), ("cfg5", workloads.cfg5_problem(DEV))]:
         mk = int(p.lens.max())
+        c = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
+                             part_tokens=DYN)
         a = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
                              part_tokens=SK)
         b = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
@@ -115,9 +122,12 @@ def test_cfg4_and_cfg5_kernels_agree():
         torch.cuda.synchronize()
         diff = (a.float() - b.float()).abs().max().item()
         assert diff <= 2e-2, f"{name}: persistent vs partition kernel differ by {diff}"
+        diff = (c.float() - b.float()).abs().max().item()
+        assert diff <= 2e-2, f"{name}: dynamic persistent vs partition kernel differ by {diff}"
     
 
-def test_records_of_previous_call_do_not_leak():
+@pytest.mark.parametrize("pt", [SK, STATIC, DYN])
+def test_records_of_previous_call_do_not_leak(pt):
     """A call where every sequence is split across workgroups, then a call on
     the same workspace where some of those sequences have no query: rows are
     written only for the queries present (a guard row past T stays intact)."""
@@ -125,7 +135,7 @@ def test_records_of_previous_call_do_not_leak():
     lens = [6000, 5000, 7000, 4000, 6500]
     p = workloads.decode_problem(lens, g, 1, d, 16, 4096, torch.bfloat16, DEV, seed=14)
     first = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens,
-                             part_tokens=SK)
+                             part_tokens=pt)
     torch.cuda.synchronize()
     eo, el = oracle(p)
     check(first, None, eo, el, "all queries")
@@ -136,10 +146,73 @@ def test_records_of_previous_call_do_not_leak():
     out = torch.full((T + 1, g, d), 7.0, dtype=torch.bfloat16, device=DEV)
     lse = torch.full((T + 1, g), 7.0, device=DEV)
     paged_mqa_decode(q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, out=out[:T],
-                     lse=lse[:T], part_tokens=SK, query_start_loc=qsl)
+                     lse=lse[:T], part_tokens=pt, query_start_loc=qsl)
     torch.cuda.synchronize()
     eo2, el2 = ref.paged_attention(np64(q), np64(p.k_pool), np64(p.v_pool),
                                    p.block_tables.cpu().numpy(), p.seq_lens.cpu().numpy(),
                                    qsl.cpu().numpy())
     check(out[:T], lse[:T], eo2, el2, "subset of queries")
     assert torch.all(out[T] == 7.0) and torch.all(lse[T] == 7.0), "guard row overwritten"
+
+
+def _counters():
+    """The dynamic persistent kernel's draw and arrival counters (first
+    8 KiB of the library workspace on this device)."""
+    buf = _native.WORKSPACE._bufs[torch.cuda.current_device()]
+    return buf[: 8 * 1024].view(torch.int32)
+
+
+def test_cut_sequences_alternating_inputs_and_counters_reset():
+    """Pieces of long sequences are merged inside the kernel by the last
+    workgroup to arrive, from partials other workgroups (on other XCDs)
+    stored just before. Two problems with the same lengths and tables but different
+    Q/K/V alternate on one workspace: a partial read before it was written
+    this call (stale, from the previous call) would carry the other
+    problem's values. Every call is checked, and the arrival counters are
+    back to zero after each."""
+    g, d = 32, 128
+    rng = np.random.default_rng(21)
+    lens = np.minimum(rng.lognormal(np.log(900), 1.0, size=96).astype(int) + 1, 6000)
+    pa = workloads.decode_problem(lens, g, 1, d, 16, 16384, torch.bfloat16, DEV, seed=21)
+    pb = workloads.decode_problem(lens, g, 1, d, 16, 16384, torch.bfloat16, DEV, seed=22)
+    pb.block_tables.copy_(pa.block_tables)
+    refs = {"a": oracle(pa), "b": oracle(pb)}
+    for i in range(12):
+        name, p = ("a", pa) if i % 2 == 0 else ("b", pb)
+        lse = torch.empty(len(lens), g, device=DEV)
+        out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, lse=lse,
+                               part_tokens=DYN)
+        torch.cuda.synchronize()
+        check(out, lse, *refs[name], f"call {i} ({name})")
+        assert int(_counters().abs().sum()) == 0, f"call {i}: arrival counters not reset"
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_persistent_random_length_mixes(seed):
+    """Random batch sizes and length mixes (a few sequences longer than a
+    share, many shorter, empty contexts, sizes where the cost line has fewer
+    units than workgroups): every way a share can start, end and be cut."""
+    rng = np.random.default_rng(100 + seed)
+    g, d = [(16, 64), (32, 128), (16, 128), (32, 64)][seed % 4]
+    n = int(rng.choice([1, 3, 40, 300, 700]))
+    kind = seed % 3
+    if kind == 0:
+        lens = rng.integers(0, 120, size=n)
+    elif kind == 1:
+        lens = np.minimum(rng.lognormal(np.log(600), 1.3, size=n).astype(int), 9000)
+    else:
+        lens = rng.integers(0, 40, size=n)
+        lens[rng.integers(0, n, size=max(1, n // 50))] = rng.integers(2000, 12000)
+    print(f"[decode mix] seed={seed} g={g} d={d} n={n} sum={int(lens.sum())}", flush=True)
+    nb = 1 << max(10, int(np.ceil(np.log2(sum((int(x) + 15) // 16 + 1 for x in lens) * 1.3))))
+    p = workloads.decode_problem(np.maximum(lens, 1), g, 1, d, 16, nb, torch.bfloat16, DEV,
+                                 seed=200 + seed)
+    seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
+    eo, el = oracle(p, seq_lens)
+    for rep in range(2):
+        lse = torch.empty(n, g, device=DEV)
+        out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
+                               part_tokens=DYN)
+        torch.cuda.synchronize()
+        check(out, lse, eo, el, f"mix seed {seed} rep {rep}")
+        assert int(_counters().abs().sum()) == 0, "arrival counters not reset"

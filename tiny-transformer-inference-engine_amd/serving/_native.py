@@ -22,8 +22,13 @@ PKV_STATUS_BAD_BLOCK = 2
 PKV_STATUS_SHORT_TABLE = 4
 PKV_STATUS_BAD_QLOC = 8
 PKV_STATUS_BAD_POS = 16
-# part_tokens value selecting the persistent (stream-K) decode kernel
+# part_tokens values selecting a persistent decode kernel: the one the
+# library prefers, the one with static equal shares, or the dynamically
+# scheduled one (largest-first work items drawn from a counter; up to 1024
+# sequence x kv head pairs and block_size >= 16, else the static one)
 PART_PERSISTENT = -1
+PART_STATIC = -2
+PART_DYNAMIC = -3
 
 _lib = None
 _lock = threading.Lock()
@@ -158,8 +163,11 @@ class Workspace:
         if buf is None or buf.numel() < nbytes:
             # grow geometrically so ragged batches do not reallocate every step
             size = max(nbytes, 0 if buf is None else 2 * buf.numel())
-            # every call writes what it reads back: no initialisation needed
-            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            # zero-filled once: the persistent decode kernel's arrival
+            # counters (the first 256 KiB) must start at zero, and every
+            # call leaves them zero; the partials are written before they
+            # are read
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
             self._bufs[idx] = buf
         return buf
 
