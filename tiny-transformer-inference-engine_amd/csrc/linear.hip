@@ -30,6 +30,7 @@ constexpr int kLW = 8;             // wavefronts per workgroup (K split)
 constexpr int kLThreads = 64 * kLW;
 constexpr int kNT = 16;            // output features per tile
 constexpr int kPitch = kNT + 1;    // LDS row pitch of the partial sums (floats)
+constexpr int kKB = 4;             // K steps per wavefront whose loads are in flight together
 
 enum { kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2 };
 
@@ -102,9 +103,7 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   const int m = m0 + ml;
   const int n = n0 + 2 * p;
   const bool live = t < MT * (kNT / 2) && m < a.m && n < a.n;
-  // rope: the row's position is requested before the operands and its
-  // table entries right after them, so neither dependent load is waited
-  // for after the reduction
+  // rope: the row's position is requested before the operands
   const int qn = a.hq * a.d;
   const int kn = a.hkv * a.d;
   const bool rot = EPI == kEpiRope && live && n < qn + kn;
@@ -124,14 +123,39 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[s][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
-  v8 av[NS], bv[MB];
+  // The wavefront's K steps in batches of kKB, every load of a batch issued
+  // before the first product (indices past the range are clamped onto its
+  // last step and their products skipped), so a batch costs one memory
+  // round trip. Each accumulator still adds its K steps in order.
+  v8 av[kKB][NS], bv[kKB][MB];
   auto load = [&](int st, v8* A, v8* B) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) A[s] = *reinterpret_cast<const v8*>(wrow[s] + st * 32);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) B[mb] = *reinterpret_cast<const v8*>(xrow[mb] + st * 32);
   };
-  if (s0 < s1) load(s0, av, bv);
+  // clamp target: the range's last step (a wavefront without steps re-reads step 0)
+  const int s_last = s0 < s1 ? s1 - 1 : 0;
+#pragma unroll
+  for (int j = 0; j < kKB; ++j) load(min(s0 + j, s_last), av[j], bv[j]);
+  for (int sb = s0; sb < s1; sb += kKB) {
+#pragma unroll
+    for (int j = 0; j < kKB; ++j) {
+      if (sb + j < s1) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[s][mb] = Ops<T>::mma(av[j][s], bv[j][mb], acc[s][mb]);
+      }
+    }
+    if (sb + kKB < s1) {
+#pragma unroll
+      for (int j = 0; j < kKB; ++j) load(min(sb + kKB + j, s_last), av[j], bv[j]);
+    }
+  }
+
+  // rope: the row's table entries, requested once the products are issued
+  // (the position was requested before the operands)
   float cj = 0.f, sj = 0.f;
   bool bad_pos = false;
   if constexpr (EPI == kEpiRope) {
@@ -146,20 +170,6 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
       const int64_t tix = (int64_t)pos * (a.d >> 1) + (c >> 1);
       cj = a.cos[tix];
       sj = a.sin[tix];
-    }
-  }
-  for (int st = s0; st < s1; ++st) {
-    v8 an[NS], bn[MB];
-    if (st + 1 < s1) load(st + 1, an, bn);
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[s][mb] = Ops<T>::mma(av[s], bv[mb], acc[s][mb]);
-    if (st + 1 < s1) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) av[s] = an[s];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) bv[mb] = bn[mb];
     }
   }
 

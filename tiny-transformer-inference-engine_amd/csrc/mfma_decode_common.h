@@ -237,18 +237,20 @@ __device__ __forceinline__ void chunk_scores(const ChunkCtx& cx,
   // the slice is private to this wavefront: waiting for its own LDS writes
   // is the only synchronisation the reads below need
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  // k-step outermost: one K fragment live at a time (each accumulator still
+  // sums its k-steps in order 0, 1, ...)
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    v8 kf[KS];
+  for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      kf[ks] = *reinterpret_cast<const v8*>(cx.kl + Geo::off(16 * h + cx.l16, 4 * ks + cx.grp));
+    for (int h = 0; h < 2; ++h) sacc[nt][h] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) acc = Ops<T>::mma(kf[ks], qf[nt][ks], acc);
-      sacc[nt][h] = acc;
+    for (int h = 0; h < 2; ++h) {
+      const v8 kf =
+          *reinterpret_cast<const v8*>(cx.kl + Geo::off(16 * h + cx.l16, 4 * ks + cx.grp));
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) sacc[nt][h] = Ops<T>::mma(kf, qf[nt][ks], sacc[nt][h]);
     }
   }
 }
