@@ -296,9 +296,16 @@ int launch_generic(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
 }
 
 template <typename T>
-int launch_mfma(const AttnArgs& a, const AttnPlan& p, int dtype, hipStream_t stream) {
+int launch_mfma(const AttnArgs& a0, const AttnPlan& p, int dtype, hipStream_t stream) {
+  AttnArgs a = a0;
+  // split sequences merged inside the decode kernel when the workspace
+  // header has a counter for every (sequence, kv head) pair
+  if (p.parts_max > 1 && p.tiles_max == 1 && a.ws_o &&
+      (int64_t)a.n_seq * a.hkv <= kMergeCtrMax)
+    a.merge_ctr = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes) +
+                  kMergeCtrOff;
   int rc = launch_decode_mfma(a, p, dtype, stream);
-  if (rc != PKV_OK || p.parts_max == 1) return rc;
+  if (rc != PKV_OK || p.parts_max == 1 || a.merge_ctr) return rc;
   return launch_merge<T>(a, p, stream);
 }
 

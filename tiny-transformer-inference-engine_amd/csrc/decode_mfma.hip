@@ -196,6 +196,21 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
       dst[2] = (T)(acc[2] * inv);
       dst[3] = (T)(acc[3] * inv);
       if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
+    } else if (a.merge_ctr) {
+      // written through to memory: the merging workgroup may sit on another
+      // XCD
+      uint64_t b0, b1;
+      __builtin_memcpy(&b0, &acc, 8);
+      __builtin_memcpy(&b1, reinterpret_cast<const char*>(&acc) + 8, 8);
+      float* po = a.ws_o + (unit * G + head) * D + d0;
+      st_agent64(po, b0);
+      st_agent64(po + 2, b1);
+      if (d0 == 0) {
+        const float2 ml = make_float2(M, L);
+        uint64_t bm;
+        __builtin_memcpy(&bm, &ml, 8);
+        st_agent64(a.ws_ml + (unit * G + head) * 2, bm);
+      }
     } else {
       *reinterpret_cast<floatx4*>(a.ws_o + (unit * G + head) * D + d0) = acc;
       if (d0 == 0) {
@@ -203,6 +218,60 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
         a.ws_ml[(unit * G + head) * 2 + 1] = L;
       }
     }
+  }
+  if (!a.merge_ctr || g.nparts == 1) return;
+
+  // ---- in-kernel split-K merge: once its partial stores have completed,
+  // each partition counts itself in; the one that brings the count to
+  // nparts merges every partition (loads issued in batches of 8 before any
+  // is consumed, as merge_kernel does), writes the rows and resets the
+  // counter for the next call. No workgroup waits for another.
+  __shared__ int s_last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* ctr = a.merge_ctr + blockIdx.x;
+    const int old = fetch_add_agent(ctr, 1);
+    s_last = old == g.nparts - 1;
+    if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int64_t unit0 = (int64_t)blockIdx.x * a.parts_max;
+  constexpr int kMB = 8;
+  for (int idx = threadIdx.x; idx < G * D / 4; idx += kBlock) {
+    const int head = idx / (D / 4);
+    const int d0 = (idx - head * (D / 4)) * 4;
+    float M = -INFINITY, L = 0.f;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int p0 = 0; p0 < g.nparts; p0 += kMB) {
+      float2 ml[kMB];
+      floatx4 oo[kMB];
+#pragma unroll
+      for (int j = 0; j < kMB; ++j) {
+        const int64_t row = (unit0 + min(p0 + j, g.nparts - 1)) * G + head;
+        ml[j] = *reinterpret_cast<const float2*>(a.ws_ml + row * 2);
+        oo[j] = *reinterpret_cast<const floatx4*>(a.ws_o + row * D + d0);
+      }
+#pragma unroll
+      for (int j = 0; j < kMB; ++j) {
+        if (p0 + j >= g.nparts || ml[j].x == -INFINITY) continue;
+        const float Mn = fmaxf(M, ml[j].x);
+        const float sa = exp2f(M - Mn);
+        const float sb = exp2f(ml[j].x - Mn);
+        L = L * sa + ml[j].y * sb;
+        acc = acc * sa + oo[j] * sb;
+        M = Mn;
+      }
+    }
+    const int64_t qrow = qrow0 + head;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    T* dst = out + qrow * D + d0;
+    dst[0] = (T)(acc[0] * inv);
+    dst[1] = (T)(acc[1] * inv);
+    dst[2] = (T)(acc[2] * inv);
+    dst[3] = (T)(acc[3] * inv);
+    if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
   }
 }
 

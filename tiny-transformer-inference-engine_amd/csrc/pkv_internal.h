@@ -104,6 +104,11 @@ struct AttnArgs {
   const void* k_new;
   const void* v_new;
   const int32_t* new_pos;
+  // split-K partition kernel: per-(sequence, kv head) arrival counters
+  // (workspace header, zero between calls); when set, the last partition
+  // of a sequence to finish merges the partials itself and no merge kernel
+  // runs
+  int* merge_ctr;
 };
 
 // Rows ((query token, head) pairs of one kv head) per tile of the generic
@@ -190,6 +195,27 @@ typedef const __attribute__((address_space(4))) int32_t scalar_i32;
 __device__ __forceinline__ int ld_meta(const int32_t* p, int64_t i) {
   return ((scalar_i32*)p)[i];
 }
+
+// Device-scope coherent accesses for data exchanged between workgroups
+// within one launch: relaxed agent-scope atomic stores (global_store with the
+// device scope bits: written through the XCD's L2), and a relaxed fetch-add
+// whose address the compiler cannot prove uniform, so it is issued as it
+// stands (not rewritten into a wavefront-wide aggregate whose result is
+// waited for at once) and as a global (not flat) access.
+__device__ __forceinline__ void st_agent64(void* p, uint64_t x) {
+  __hip_atomic_store(static_cast<uint64_t*>(p), x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+typedef __attribute__((address_space(1))) int global_i32;
+__device__ __forceinline__ int fetch_add_agent(int* p, int x) {
+  global_i32* g = (global_i32*)p;
+  asm volatile("" : "+v"(g));
+  return __hip_atomic_fetch_add(g, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Counters of the split-K partition kernel's in-kernel merge, one per
+// (sequence, kv head) pair, after the dynamic kernel's in the header.
+constexpr int kMergeCtrOff = 1 + kDynMaxSeq;
+constexpr int kMergeCtrMax = (int)(kWsDynCtrBytes / sizeof(int)) - kMergeCtrOff;
 
 __device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
                                           int rows_per_tile, TileGeom& g) {
