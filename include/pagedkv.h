@@ -45,6 +45,14 @@
  *   pkv_linear_swiglu     gate_proj, up_proj and fused_swiglu
  *                                                    models/mlp.py:24-30
  *   pkv_linear_rope_qkv   q/k/v projections and RoPE serving/paged_mqa.py:76-85
+ *   pkv_linear_residual   x + out(attn) / x + down_proj(...) of PagedBlock.forward
+ *                                                    serving/paged_model.py:20-29
+ *   pkv_linear_swiglu_rmsnorm  mlp_norm + gate_proj, up_proj, fused_swiglu
+ *                                                    serving/paged_model.py:28-29,
+ *                                                    models/rmsnorm.py:12-18, models/mlp.py:24-30
+ *   pkv_linear_rope_qkv_rmsnorm  attn_norm + q/k/v projections and RoPE
+ *                                                    serving/paged_model.py:26-27,
+ *                                                    models/rmsnorm.py:12-18, serving/paged_mqa.py:76-85
  *   pkv_argmax_rows       greedy token choice: logits.argmax per sequence
  *                                                    serving/generation.py:77,88,132,142;
  *                         greedy()                   sampling.py:5-137
@@ -273,7 +281,7 @@ int pkv_silu_mul(void* out, const void* gate, const void* up, int64_t rows, int6
  * rows 16-byte aligned (PKV_ERR_UNSUPPORTED otherwise, as for fp32). Built
  * for decode steps (m up to a few hundred): the workgroups split k, so the
  * weight is streamed by the whole chip. The sum order is fixed: results are
- * deterministic and identical across the three pkv_linear* entry points.
+ * deterministic and identical across the pkv_linear* entry points.
  * Replaces nn.Linear for the out projection (serving/paged_mqa.py:112-113)
  * and down_proj (models/mlp.py:31-32).
  */
@@ -307,6 +315,43 @@ int pkv_linear_rope_qkv(void* q_out, void* k_out, void* v_out, const void* x, co
                         const int32_t* positions, const float* cos_table,
                         const float* sin_table, int max_pos, int hq, int hkv, int d, int dtype,
                         int* status, void* stream);
+
+/*
+ * Residual projection: resid [m, n] (contiguous) += x W^T (+ bias), the
+ * projection rounded to dtype first and the sum rounded (bit-identical to
+ * pkv_linear followed by an element-wise add in dtype). Same requirements as
+ * pkv_linear. Replaces the residual adds of PagedBlock.forward around the
+ * out projection and down_proj (serving/paged_model.py:20-29).
+ */
+int pkv_linear_residual(void* resid, const void* x, const void* w, const void* bias, int64_t m,
+                        int64_t n, int64_t k, int64_t x_stride, int dtype, void* stream);
+
+/*
+ * pkv_linear_swiglu of RMSNorm(x): the rows of x are normalised in the
+ * kernel, (x * rsqrt(mean(x^2) + eps)) * norm_weight[k] in fp32 rounded to
+ * dtype, before the products. Bit-identical to pkv_rms_norm followed by
+ * pkv_linear_swiglu (both take the sum of squares in the same fixed order).
+ * Needs k <= 1024 (PKV_ERR_UNSUPPORTED otherwise) and a 16-byte aligned
+ * norm_weight; else as pkv_linear_swiglu. Replaces mlp_norm followed by
+ * the MLP front half (serving/paged_model.py:28-29, models/rmsnorm.py:12-18,
+ * models/mlp.py:24-30).
+ */
+int pkv_linear_swiglu_rmsnorm(void* out, const void* x, const void* norm_weight, float eps,
+                              const void* w_gate_up, const void* bias, int64_t m, int64_t n,
+                              int64_t k, int64_t x_stride, int dtype, void* stream);
+
+/*
+ * pkv_linear_rope_qkv of RMSNorm(x), normalised as in
+ * pkv_linear_swiglu_rmsnorm (bit-identical to pkv_rms_norm followed by
+ * pkv_linear_rope_qkv). Same requirements as those two. Replaces attn_norm
+ * followed by serving/paged_mqa.py:76-85 (serving/paged_model.py:26-27).
+ */
+int pkv_linear_rope_qkv_rmsnorm(void* q_out, void* k_out, void* v_out, const void* x,
+                                const void* norm_weight, float eps, const void* w_qkv,
+                                const void* bias, int64_t m, int64_t k, int64_t x_stride,
+                                const int32_t* positions, const float* cos_table,
+                                const float* sin_table, int max_pos, int hq, int hkv, int d,
+                                int dtype, int* status, void* stream);
 
 /*
  * Greedy token choice: ids[r] (int64) = the index of the largest of the

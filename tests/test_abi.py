@@ -91,6 +91,15 @@ def test_linear_validation_without_gpu():
     assert L.pkv_linear(None, 16, 16, None, 4, 8, 64, 64, 2, None) == -1
     assert L.pkv_linear(16, 16, 16, None, 4, 8, 64, 32, 2, None) == -1  # x_stride < k
     assert L.pkv_linear_swiglu(16, 16, 16, None, 4, 8, 48, 48, 1, None) == -2
+    assert L.pkv_linear_residual(16, 16, 16, None, 4, 8, 64, 64, 0, None) == -2
+    assert L.pkv_linear_residual(16, 16, 16, None, 4, 8, 64, 32, 2, None) == -1
+    # the fused norm: k above 1024 refused before any launch, norm weight checked
+    assert L.pkv_linear_swiglu_rmsnorm(16, 16, 16, 1e-5, 16, None, 4, 8, 1056, 1056, 2,
+                                       None) == -2
+    assert L.pkv_linear_swiglu_rmsnorm(16, 16, None, 1e-5, 16, None, 4, 8, 64, 64, 2,
+                                       None) == -1
+    assert L.pkv_linear_rope_qkv_rmsnorm(16, 16, 16, 16, 8, 1e-5, 16, None, 4, 64, 64, 16, 16,
+                                         16, 8, 4, 1, 8, 2, None, None) == -1
     # odd head dim, missing tables
     assert L.pkv_linear_rope_qkv(16, 16, 16, 16, 16, None, 4, 64, 64, 16, 16, 16, 8, 4, 1, 7,
                                  2, None, None) == -1

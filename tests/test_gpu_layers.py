@@ -126,7 +126,8 @@ def rms_ref32(x, w, eps):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,dim,strided", [(1, 128, False), (128, 1024, False),
-                                              (7, 4096, True), (5, 1000, False), (3, 12, True)])
+                                              (7, 4096, True), (5, 1000, False), (3, 12, True),
+                                              (2, 8192, False), (2, 9216, True), (4, 96, False)])
 def test_rms_norm_vs_fp32_formula(dtype, rows, dim, strided):
     print(f"[rms_norm] {dtype} rows={rows} dim={dim} strided={strided}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(rows * dim)

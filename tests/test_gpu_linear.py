@@ -11,6 +11,13 @@
   pkv_linear_rope_qkv  bit-identical to pkv_linear followed by the
                        stand-alone RoPE kernel on the three column ranges;
                        a position past the tables sets PKV_STATUS_BAD_POS.
+  pkv_linear_residual  bit-identical to pkv_linear followed by the
+                       framework add (resid + y rounded to the dtype).
+  pkv_linear_swiglu_rmsnorm, pkv_linear_rope_qkv_rmsnorm
+                       bit-identical to pkv_rms_norm followed by the
+                       unfused projection (the prologue sums squares in the
+                       stand-alone kernel's order); k above 1024 is refused
+                       by the library and composed by the wrappers.
   Determinism          two launches give identical bits.
 """
 import math
@@ -144,3 +151,96 @@ def test_linear_rope_position_past_table_flags_status():
     assert rc == 0
     torch.cuda.synchronize()
     assert int(status.item()) == _native.PKV_STATUS_BAD_POS
+
+
+def _first_diff(got, expect):
+    bad = (got != expect).nonzero()
+    if not len(bad):
+        return None
+    idx = tuple(int(v) for v in bad[0])
+    return (f"{len(bad)} of {got.numel()} differ; first at {idx}: fused {got[idx].item()!r} "
+            f"two-step {expect[idx].item()!r}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k,bias,strided", [(128, 1024, 1024, False, False),
+                                                (1, 64, 32, True, False),
+                                                (17, 1000, 2816, False, True),
+                                                (256, 48, 96, True, False)])
+def test_linear_residual_equals_linear_then_add(dtype, m, n, k, bias, strided):
+    print(f"[linear_residual] {dtype} m={m} n={n} k={k} bias={bias}", flush=True)
+    base = rand((m, k + (64 if strided else 0)), dtype, 41)
+    x = base[:, 32:32 + k] if strided else base
+    w = rand((n, k), dtype, 42, scale=0.05)
+    b = rand((n,), dtype, 43) if bias else None
+    resid = rand((m, n), dtype, 44, scale=4.0)
+    expect = resid + fused_ops.linear(x, w, b)
+    got = resid.clone()
+    out = fused_ops.linear_residual_(got, x, w, b)
+    torch.cuda.synchronize()
+    assert out is got
+    msg = _first_diff(got, expect)
+    assert msg is None, msg
+
+
+def _norm_inputs(dtype, m, k, seed, strided):
+    base = rand((m, k + (64 if strided else 0)), dtype, seed, scale=3.0)
+    x = base[:, 32:32 + k] if strided else base
+    g = torch.Generator(device=DEV).manual_seed(seed + 1)
+    nw = (1.0 + 0.2 * torch.randn(k, generator=g, device=DEV)).to(dtype)
+    return x, nw
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,h,k,bias,strided", [(128, 2816, 1024, False, False),
+                                                (1, 100, 32, True, False),
+                                                (7, 256, 96, False, True),
+                                                (64, 512, 640, True, False)])
+def test_linear_swiglu_rmsnorm_equals_norm_then_projection(dtype, m, h, k, bias, strided):
+    print(f"[linear_swiglu_rmsnorm] {dtype} m={m} h={h} k={k}", flush=True)
+    x, nw = _norm_inputs(dtype, m, k, 51, strided)
+    w = rand((2 * h, k), dtype, 52, scale=0.1)
+    b = rand((2 * h,), dtype, 53) if bias else None
+    got = fused_ops.linear_swiglu_rmsnorm(x, nw, 1e-5, w, b)
+    expect = fused_ops.linear_swiglu(fused_ops.rms_norm(x, nw, 1e-5), w, b)
+    torch.cuda.synchronize()
+    msg = _first_diff(got, expect)
+    assert msg is None, msg
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,hq,hkv,d,k,bias,strided", [(128, 16, 1, 64, 1024, False, False),
+                                                       (9, 4, 2, 128, 512, True, True),
+                                                       (1, 8, 1, 64, 64, False, False)])
+def test_linear_rope_qkv_rmsnorm_equals_norm_then_projection(dtype, m, hq, hkv, d, k, bias,
+                                                             strided):
+    print(f"[linear_rope_qkv_rmsnorm] {dtype} m={m} hq={hq} hkv={hkv} d={d} k={k}", flush=True)
+    n = (hq + 2 * hkv) * d
+    x, nw = _norm_inputs(dtype, m, k, 61, strided)
+    w = rand((n, k), dtype, 62, scale=0.1)
+    b = rand((n,), dtype, 63) if bias else None
+    rope = RoPE(d, max_seq_len=4096).to(DEV)
+    cos, sin = rope._tables_fp32()
+    pos = torch.randint(0, 4096, (m,), device=DEV, dtype=torch.int32)
+    got = fused_ops.linear_rope_qkv_rmsnorm(x, nw, 1e-6, w, b, pos, cos, sin, hq, hkv, d)
+    expect = fused_ops.linear_rope_qkv(fused_ops.rms_norm(x, nw, 1e-6), w, b, pos, cos, sin,
+                                       hq, hkv, d)
+    torch.cuda.synchronize()
+    for g_, e_ in zip(got, expect):
+        msg = _first_diff(g_, e_)
+        assert msg is None, msg
+
+
+def test_fused_norm_past_1024_features_refused_then_composed():
+    m, h, k = 4, 64, 1056
+    x, nw = _norm_inputs(torch.bfloat16, m, k, 71, False)
+    w = rand((2 * h, k), torch.bfloat16, 72, scale=0.1)
+    out = torch.empty((m, h), dtype=torch.bfloat16, device=DEV)
+    rc = _native.lib().pkv_linear_swiglu_rmsnorm(
+        out.data_ptr(), x.data_ptr(), nw.data_ptr(), 1e-5, w.data_ptr(), None, m, h, k, k,
+        _native.dtype_code(torch.bfloat16), _native.stream_ptr(x.device))
+    assert rc == _native.PKV_ERR_UNSUPPORTED
+    got = fused_ops.linear_swiglu_rmsnorm(x, nw, 1e-5, w, None)
+    expect = fused_ops.linear_swiglu(fused_ops.rms_norm(x, nw, 1e-5), w, None)
+    torch.cuda.synchronize()
+    assert torch.equal(got, expect)

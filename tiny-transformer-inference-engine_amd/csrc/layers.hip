@@ -74,10 +74,14 @@ struct RmsArgs {
 
 constexpr int kRmsMaxWaves = 4;
 
-// one workgroup per row; pass 1 forms the residual sum (stored) and the sum
-// of squares, pass 2 re-reads the row (now in cache) and writes the output
+// one workgroup per row; pass 1 forms the residual sum (stored) and keeps the
+// row in LDS, the sum of squares is taken in the fixed order of kNormSplit
+// ranges (the order the projection kernel's fused norm uses), pass 2 writes
+// the output. Rows whose length is not a multiple of 32 (or above
+// kNormCanonMax) use a plain strided sum instead.
 template <typename T, int V>
 __global__ __launch_bounds__(64 * kRmsMaxWaves) void rms_norm_kernel(RmsArgs a) {
+#pragma clang fp contract(off)
   const int64_t row = blockIdx.x;
   const T* x = static_cast<const T*>(a.x) + row * a.x_stride;
   const T* h = a.delta ? static_cast<const T*>(a.delta) + row * a.delta_stride : nullptr;
@@ -85,6 +89,10 @@ __global__ __launch_bounds__(64 * kRmsMaxWaves) void rms_norm_kernel(RmsArgs a) 
   T* y = static_cast<T*>(a.y) + row * a.dim;
   const T* w = static_cast<const T*>(a.weight);
   const int step = blockDim.x * V;
+  __shared__ float xs[kNormCanonMax];
+  __shared__ float gp[4 * kNormSplit];
+  __shared__ float part[kRmsMaxWaves];
+  const bool canon = a.dim % 32 == 0 && a.dim <= kNormCanonMax;
 
   float ss = 0.f;
   for (int i = threadIdx.x * V; i < a.dim; i += step) {
@@ -98,23 +106,52 @@ __global__ __launch_bounds__(64 * kRmsMaxWaves) void rms_norm_kernel(RmsArgs a) 
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       const float f = (float)xv.e[e];
-      ss += f * f;
+      if (canon) xs[i + e] = f;
+      ss = ss + f * f;
     }
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-  __shared__ float part[kRmsMaxWaves];
-  const int wv = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) part[wv] = ss;
-  __syncthreads();
   float tot = 0.f;
-  const int nw = blockDim.x >> 6;
-  for (int k = 0; k < nw; ++k) tot += part[k];
+  if (canon) {
+    __syncthreads();
+    if (threadIdx.x < 4 * kNormSplit) {
+      const int rg = threadIdx.x >> 2;  // range
+      const int g = threadIdx.x & 3;    // 8-element group
+      const int steps = a.dim >> 5;
+      const int per = (steps + kNormSplit - 1) / kNormSplit;
+      const int st1 = min((rg + 1) * per, steps);
+      float acc = 0.f;
+      for (int st = rg * per; st < st1; ++st)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = xs[32 * st + 8 * g + e];
+          acc = acc + f * f;
+        }
+      gp[threadIdx.x] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rg = 0; rg < kNormSplit; ++rg)
+      tot = tot + ((gp[4 * rg] + gp[4 * rg + 1]) + (gp[4 * rg + 2] + gp[4 * rg + 3]));
+  } else {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) part[wv] = ss;
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    for (int k = 0; k < nw; ++k) tot += part[k];
+  }
   const float inv = rsqrtf(tot / (float)a.dim + a.eps);
 
   const T* src = h ? r : x;
   for (int i = threadIdx.x * V; i < a.dim; i += step) {
-    const Pack<T, V> xv = ld<T, V>(src + i);
+    Pack<T, V> xv;
+    if (canon) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) xv.e[e] = (T)xs[i + e];
+    } else {
+      xv = ld<T, V>(src + i);
+    }
     const Pack<T, V> wv8 = ld<T, V>(w + i);
     Pack<T, V> out;
 #pragma unroll

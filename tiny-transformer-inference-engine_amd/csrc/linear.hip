@@ -9,6 +9,16 @@
 //           q and k rotated at positions[m], written contiguous, v copied
 //           (models/rope.py:21-47 on serving/paged_mqa.py:76-85's outputs);
 //           the rotation rounds exactly as the stand-alone RoPE kernel does.
+//   resid   out is the residual stream, updated in place: out = out + y, y
+//           rounded first and the sum rounded (PagedBlock's x + attn(...) and
+//           x + mlp(...), serving/paged_model.py:20-29).
+// and optionally the RMSNorm in front of the projection fused into its
+// prologue (NORM): the rows are the residual stream, normalised as
+// (x * rsqrt(mean(x^2) + eps)) * g in fp32 and rounded before the products
+// (models/rmsnorm.py:13-17). The sum of squares is taken in one fixed order
+// (each K-split wavefront's lane sums its 8-element groups step by step, the
+// four groups of a row pairwise, the wavefronts in order), the order the
+// stand-alone RMSNorm kernel uses too, so both give identical bits.
 //
 // With tokens in the tens to hundreds, a decode projection is a stream of
 // the weight matrix, and the library GEMMs' large output tiles leave most of
@@ -26,13 +36,13 @@ namespace {
 
 using namespace mfma;
 
-constexpr int kLW = 8;             // wavefronts per workgroup (K split)
+constexpr int kLW = kNormSplit;    // wavefronts per workgroup (K split)
 constexpr int kLThreads = 64 * kLW;
 constexpr int kNT = 16;            // output features per tile
 constexpr int kPitch = kNT + 1;    // LDS row pitch of the partial sums (floats)
 constexpr int kKB = 4;             // K steps per wavefront whose loads are in flight together
 
-enum { kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2 };
+enum { kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2, kEpiResid = 3 };
 
 struct LinArgs {
   void* out;          // plain / swiglu: [m, n] contiguous
@@ -57,6 +67,9 @@ struct LinArgs {
   int hkv;
   int d;
   int* status;
+  // fused RMSNorm prologue
+  const void* norm_w;  // [k]
+  float eps;
 };
 
 template <typename T>
@@ -64,13 +77,14 @@ __device__ __forceinline__ float rnd(float x) {
   return (float)(T)fp32_value(x);
 }
 
-template <typename T, int MB, int EPI>
+template <typename T, int MB, int EPI, bool NORM>
 __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
 #pragma clang fp contract(off)
   using v8 = typename Ops<T>::v8;
   constexpr int MT = 16 * MB;
   constexpr int NS = EPI == kEpiSwiglu ? 2 : 1;  // weight row sets (gate, up)
   __shared__ float red[NS][kLW][MT][kPitch];
+  __shared__ float rsum[NORM ? kLW : 1][MT];
 
   const int b = blockIdx.x;
   const int xcd = b & 7;
@@ -138,6 +152,53 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   const int s_last = s0 < s1 ? s1 - 1 : 0;
 #pragma unroll
   for (int j = 0; j < kKB; ++j) load(min(s0 + j, s_last), av[j], bv[j]);
+  if constexpr (NORM) {
+    // the whole K range of this wavefront is in registers (the host keeps
+    // k within kLW * kKB steps): the rows' sums of squares, then the
+    // normalised operands. Lane: row 16 mb + l16, elements 32 st + 8 (lane
+    // >> 4) + e of its steps st.
+    const T* gw = static_cast<const T*>(a.norm_w) + (lane >> 4) * 8;
+    v8 gv[kKB];
+#pragma unroll
+    for (int j = 0; j < kKB; ++j) gv[j] = *reinterpret_cast<const v8*>(gw + min(s0 + j, s_last) * 32);
+    float inv[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < kKB; ++j) {
+        if (s0 + j < s1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float f = (float)bv[j][mb][e];
+            ss = ss + f * f;
+          }
+        }
+      }
+      ss = head_lanes_sum(ss);  // (g0 + g1) + (g2 + g3) over the row's 4 lane groups
+      if ((lane >> 4) == 0) rsum[w][16 * mb + l16] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      float tot = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kLW; ++ww) tot = tot + rsum[ww][16 * mb + l16];
+      inv[mb] = rsqrtf(tot / (float)a.k + a.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < kKB; ++j)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        // convert the operand again rather than keep the fp32 values of the
+        // square sums alive across the barrier (64 more registers, which
+        // would halve the workgroups a CU holds)
+        asm volatile("" : "+v"(bv[j][mb]));
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          bv[j][mb][e] = (T)fp32_value(((float)bv[j][mb][e] * inv[mb]) * (float)gv[j][e]);
+      }
+  }
   for (int sb = s0; sb < s1; sb += kKB) {
 #pragma unroll
     for (int j = 0; j < kKB; ++j) {
@@ -207,6 +268,10 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
     T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
     o[0] = (T)v[0][0];
     if (two) o[1] = (T)v[0][1];
+  } else if constexpr (EPI == kEpiResid) {
+    T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
+    o[0] = (T)fp32_value((float)o[0] + rnd<T>(v[0][0]));
+    if (two) o[1] = (T)fp32_value((float)o[1] + rnd<T>(v[0][1]));
   } else if constexpr (EPI == kEpiSwiglu) {
     T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
 #pragma unroll
@@ -236,7 +301,7 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   }
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, bool NORM>
 int launch_t(LinArgs a, hipStream_t stream) {
   const int mb = a.m <= 16 ? 1 : 2;
   a.m_tiles = (a.m + 16 * mb - 1) / (16 * mb);
@@ -244,18 +309,21 @@ int launch_t(LinArgs a, hipStream_t stream) {
   const int64_t blocks = (int64_t)((a.n_tiles + 7) / 8) * 8 * a.m_tiles;
   if (blocks > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "linear: %lld tiles", (long long)blocks);
   if (mb == 1)
-    hipLaunchKernelGGL((linear_kernel<T, 1, EPI>), dim3((unsigned)blocks), dim3(kLThreads), 0,
-                       stream, a);
+    hipLaunchKernelGGL((linear_kernel<T, 1, EPI, NORM>), dim3((unsigned)blocks), dim3(kLThreads),
+                       0, stream, a);
   else
-    hipLaunchKernelGGL((linear_kernel<T, 2, EPI>), dim3((unsigned)blocks), dim3(kLThreads), 0,
-                       stream, a);
+    hipLaunchKernelGGL((linear_kernel<T, 2, EPI, NORM>), dim3((unsigned)blocks), dim3(kLThreads),
+                       0, stream, a);
   return check_launch("linear_kernel");
 }
 
-template <int EPI>
+template <int EPI, bool NORM = false>
 int dispatch(const LinArgs& a, int dtype, hipStream_t stream) {
-  if (dtype == PKV_DTYPE_BF16) return launch_t<bf16, EPI>(a, stream);
-  if (dtype == PKV_DTYPE_F16) return launch_t<f16, EPI>(a, stream);
+  if (NORM && (a.k >> 5) > kLW * kKB)
+    return fail(PKV_ERR_UNSUPPORTED, "linear: fused RMSNorm needs k <= %d (got %d)",
+                kLW * kKB * 32, a.k);
+  if (dtype == PKV_DTYPE_BF16) return launch_t<bf16, EPI, NORM>(a, stream);
+  if (dtype == PKV_DTYPE_F16) return launch_t<f16, EPI, NORM>(a, stream);
   return fail(PKV_ERR_UNSUPPORTED, "linear: dtype %d (bf16 / fp16 only)", dtype);
 }
 
@@ -275,6 +343,51 @@ int check_common(const void* out, const void* x, const void* w, int64_t m, int64
   return PKV_OK;
 }
 
+}  // namespace
+}  // namespace pkv
+
+namespace pkv {
+namespace {
+// q/k/v projection with RoPE, optionally with the RMSNorm fused in front
+// (norm_weight non-null)
+int rope_qkv(void* q_out, void* k_out, void* v_out, const void* x, const void* norm_weight,
+             float eps, const void* w_qkv, const void* bias, int64_t m, int64_t k,
+             int64_t x_stride, const int32_t* positions, const float* cos_table,
+             const float* sin_table, int max_pos, int hq, int hkv, int d, int dtype, int* status,
+             void* stream) {
+  if (hq <= 0 || hkv <= 0 || d <= 0 || (d & 1) || max_pos <= 0)
+    return fail(PKV_ERR_INVALID, "linear_rope_qkv: bad sizes hq=%d hkv=%d d=%d max_pos=%d", hq,
+                hkv, d, max_pos);
+  const int64_t n = (int64_t)(hq + 2 * hkv) * d;
+  const int rc = check_common(q_out, x, w_qkv, m, n, k, x_stride, dtype);
+  if (rc != PKV_OK) return rc;
+  if (!k_out || !v_out || !positions || !cos_table || !sin_table)
+    return fail(PKV_ERR_INVALID, "linear_rope_qkv: null pointer argument");
+  if (m == 0) return PKV_OK;
+  LinArgs a{};
+  a.x = x;
+  a.w = w_qkv;
+  a.bias = bias;
+  a.x_stride = x_stride;
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.v_out = v_out;
+  a.positions = positions;
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.max_pos = max_pos;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.d = d;
+  a.status = status;
+  a.norm_w = norm_weight;
+  a.eps = eps;
+  if (norm_weight) return dispatch<kEpiRope, true>(a, dtype, static_cast<hipStream_t>(stream));
+  return dispatch<kEpiRope>(a, dtype, static_cast<hipStream_t>(stream));
+}
 }  // namespace
 }  // namespace pkv
 
@@ -315,40 +428,65 @@ int pkv_linear_swiglu(void* out, const void* x, const void* w_gate_up, const voi
   return dispatch<kEpiSwiglu>(a, dtype, static_cast<hipStream_t>(stream));
 }
 
-int pkv_linear_rope_qkv(void* q_out, void* k_out, void* v_out, const void* x, const void* w_qkv,
-                        const void* bias, int64_t m, int64_t k, int64_t x_stride,
-                        const int32_t* positions, const float* cos_table,
-                        const float* sin_table, int max_pos, int hq, int hkv, int d, int dtype,
-                        int* status, void* stream) {
-  if (hq <= 0 || hkv <= 0 || d <= 0 || (d & 1) || max_pos <= 0)
-    return fail(PKV_ERR_INVALID, "linear_rope_qkv: bad sizes hq=%d hkv=%d d=%d max_pos=%d", hq,
-                hkv, d, max_pos);
-  const int64_t n = (int64_t)(hq + 2 * hkv) * d;
-  const int rc = check_common(q_out, x, w_qkv, m, n, k, x_stride, dtype);
-  if (rc != PKV_OK) return rc;
-  if (!k_out || !v_out || !positions || !cos_table || !sin_table)
-    return fail(PKV_ERR_INVALID, "linear_rope_qkv: null pointer argument");
-  if (m == 0) return PKV_OK;
+int pkv_linear_residual(void* resid, const void* x, const void* w, const void* bias, int64_t m,
+                        int64_t n, int64_t k, int64_t x_stride, int dtype, void* stream) {
+  const int rc = check_common(resid, x, w, m, n, k, x_stride, dtype);
+  if (rc != PKV_OK || m == 0) return rc;
   LinArgs a{};
+  a.out = resid;
   a.x = x;
-  a.w = w_qkv;
+  a.w = w;
   a.bias = bias;
   a.x_stride = x_stride;
   a.m = (int)m;
   a.n = (int)n;
   a.k = (int)k;
-  a.q_out = q_out;
-  a.k_out = k_out;
-  a.v_out = v_out;
-  a.positions = positions;
-  a.cos = cos_table;
-  a.sin = sin_table;
-  a.max_pos = max_pos;
-  a.hq = hq;
-  a.hkv = hkv;
-  a.d = d;
-  a.status = status;
-  return dispatch<kEpiRope>(a, dtype, static_cast<hipStream_t>(stream));
+  return dispatch<kEpiResid>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+int pkv_linear_swiglu_rmsnorm(void* out, const void* x, const void* norm_weight, float eps,
+                              const void* w_gate_up, const void* bias, int64_t m, int64_t n,
+                              int64_t k, int64_t x_stride, int dtype, void* stream) {
+  int rc = check_common(out, x, w_gate_up, m, n, k, x_stride, dtype);
+  if (rc != PKV_OK) return rc;
+  if (!norm_weight || ((uintptr_t)norm_weight & 15))
+    return fail(PKV_ERR_INVALID, "linear_swiglu_rmsnorm: norm weight null or not 16-byte aligned");
+  if (m == 0) return PKV_OK;
+  LinArgs a{};
+  a.out = out;
+  a.x = x;
+  a.w = w_gate_up;
+  a.bias = bias;
+  a.x_stride = x_stride;
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
+  a.norm_w = norm_weight;
+  a.eps = eps;
+  return dispatch<kEpiSwiglu, true>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+int pkv_linear_rope_qkv_rmsnorm(void* q_out, void* k_out, void* v_out, const void* x,
+                                const void* norm_weight, float eps, const void* w_qkv,
+                                const void* bias, int64_t m, int64_t k, int64_t x_stride,
+                                const int32_t* positions, const float* cos_table,
+                                const float* sin_table, int max_pos, int hq, int hkv, int d,
+                                int dtype, int* status, void* stream) {
+  if (!norm_weight || ((uintptr_t)norm_weight & 15))
+    return fail(PKV_ERR_INVALID, "linear_rope_qkv_rmsnorm: norm weight null or not 16-byte aligned");
+  return rope_qkv(q_out, k_out, v_out, x, norm_weight, eps, w_qkv, bias, m, k, x_stride, positions,
+                  cos_table, sin_table, max_pos, hq, hkv, d, dtype, status, stream);
+}
+
+int pkv_linear_rope_qkv(void* q_out, void* k_out, void* v_out, const void* x, const void* w_qkv,
+                        const void* bias, int64_t m, int64_t k, int64_t x_stride,
+                        const int32_t* positions, const float* cos_table,
+                        const float* sin_table, int max_pos, int hq, int hkv, int d, int dtype,
+                        int* status, void* stream) {
+  return rope_qkv(q_out, k_out, v_out, x, nullptr, 0.f, w_qkv, bias, m, k, x_stride, positions,
+                  cos_table, sin_table, max_pos, hq, hkv, d, dtype, status, stream);
 }
 
 }  // extern "C"
+
+

@@ -43,6 +43,17 @@ __device__ __forceinline__ float swiglu_gate(float g, float u) {
   return fp32_value(g * sig * u);
 }
 
+// RMSNorm's sum of squares over a row of k elements (k a multiple of 32, at
+// most kNormCanonMax) is taken in one fixed order, shared by the
+// stand-alone RMSNorm kernel and the projection kernel's fused norm (whose
+// K split over kNormSplit wavefronts defines it): the 32-element steps are
+// cut into kNormSplit contiguous ranges of ceil(steps / kNormSplit) steps;
+// in each range the four 8-element groups of a step are summed separately,
+// step by step, element by element, from 0; the groups are combined as
+// (g0 + g1) + (g2 + g3) and the ranges added in order, from 0.
+constexpr int kNormSplit = 8;
+constexpr int kNormCanonMax = 8192;
+
 // ---------------------------------------------------------------------------
 // Append / gather (append.hip)
 // ---------------------------------------------------------------------------

@@ -17,6 +17,11 @@ LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libpagedkv.so")
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
+PKV_ERR_INVALID = -1
+PKV_ERR_UNSUPPORTED = -2
+PKV_ERR_WORKSPACE = -3
+PKV_ERR_HIP = -4
+
 PKV_STATUS_BAD_SLOT = 1
 PKV_STATUS_BAD_BLOCK = 2
 PKV_STATUS_SHORT_TABLE = 4
@@ -76,6 +81,13 @@ _SIGNATURES = {
     "pkv_linear_rope_qkv": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                              _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                              _c_vp, _c_vp], _c_int),
+    "pkv_linear_residual": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+                             _c_vp], _c_int),
+    "pkv_linear_swiglu_rmsnorm": ([_c_vp, _c_vp, _c_vp, _c_float, _c_vp, _c_vp, _c_i64, _c_i64,
+                                   _c_i64, _c_i64, _c_int, _c_vp], _c_int),
+    "pkv_linear_rope_qkv_rmsnorm": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_float, _c_vp, _c_vp,
+                                     _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int, _c_int,
+                                     _c_int, _c_int, _c_int, _c_vp, _c_vp], _c_int),
     "pkv_argmax_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp], _c_int),
 }
 

@@ -246,6 +246,87 @@ def linear_rope_qkv(x: torch.Tensor, w_qkv: torch.Tensor, b_qkv: torch.Tensor | 
     return q, k, v
 
 
+# the projection kernels normalise rows of at most this many features in
+# their prologue (pkv_linear_*_rmsnorm); wider rows take rms_norm first
+LINEAR_NORM_MAX_K = 1024
+
+
+def _norm_ok(x2: torch.Tensor, norm_weight: torch.Tensor) -> bool:
+    return (x2.shape[1] <= LINEAR_NORM_MAX_K and norm_weight.dtype == x2.dtype
+            and norm_weight.is_contiguous() and norm_weight.numel() == x2.shape[1]
+            and norm_weight.data_ptr() % 16 == 0)
+
+
+def linear_residual_(resid: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                     bias: torch.Tensor | None = None) -> torch.Tensor:
+    """resid += x W^T + b in place, the projection rounded to resid.dtype
+    before the add (the residual adds of serving/paged_model.py:20-29, one
+    kernel for the projection and the add). resid must be contiguous with
+    x's rows. Returns resid."""
+    x2 = _as_rows(x)
+    n = weight.shape[0]
+    if (not _linear_ok(x2, weight, bias, n) or not resid.is_contiguous()
+            or resid.dtype != x.dtype or resid.numel() != x2.shape[0] * n):
+        return resid.add_(linear(x, weight, bias).view(resid.shape))
+    rc = _native.lib().pkv_linear_residual(
+        resid.data_ptr(), x2.data_ptr(), weight.data_ptr(), _native.ptr(bias), x2.shape[0], n,
+        x2.shape[1], _x_stride(x2), _native.dtype_code(x.dtype), _native.stream_ptr(x.device))
+    _native.check(rc, "linear_residual_")
+    return resid
+
+
+def linear_swiglu_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                          w_gate_up: torch.Tensor, b_gate_up: torch.Tensor | None):
+    """linear_swiglu(rms_norm(x, norm_weight, eps), ...) with the norm taken
+    in the projection kernel's prologue (bit-identical to the two calls)."""
+    x2 = _as_rows(x)
+    h = w_gate_up.shape[0] // 2
+    if not (_linear_ok(x2, w_gate_up, b_gate_up, 2 * h) and _norm_ok(x2, norm_weight)):
+        return linear_swiglu(rms_norm(x, norm_weight, eps), w_gate_up, b_gate_up)
+    _native.require_device(x2, norm_weight, w_gate_up, what="linear_swiglu_rmsnorm")
+    out = torch.empty((x2.shape[0], h), dtype=x.dtype, device=x.device)
+    rc = _native.lib().pkv_linear_swiglu_rmsnorm(
+        out.data_ptr(), x2.data_ptr(), norm_weight.data_ptr(), float(eps), w_gate_up.data_ptr(),
+        _native.ptr(b_gate_up), x2.shape[0], h, x2.shape[1], _x_stride(x2),
+        _native.dtype_code(x.dtype), _native.stream_ptr(x.device))
+    _native.check(rc, "linear_swiglu_rmsnorm")
+    return out.view(*x.shape[:-1], h)
+
+
+def linear_rope_qkv_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                            w_qkv: torch.Tensor, b_qkv: torch.Tensor | None,
+                            positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                            hq: int, hkv: int, d: int):
+    """linear_rope_qkv(rms_norm(x, norm_weight, eps), ...) with the norm
+    taken in the projection kernel's prologue (bit-identical to the two
+    calls)."""
+    x2 = _as_rows(x)
+    T = x2.shape[0]
+    nq, nk = hq * d, hkv * d
+    if not (_linear_ok(x2, w_qkv, b_qkv, nq + 2 * nk) and _norm_ok(x2, norm_weight)):
+        return linear_rope_qkv(rms_norm(x, norm_weight, eps), w_qkv, b_qkv, positions, cos, sin,
+                               hq, hkv, d)
+    _native.require_device(x2, norm_weight, w_qkv, positions, cos, sin,
+                           what="linear_rope_qkv_rmsnorm")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError("linear_rope_qkv_rmsnorm: cos / sin must be fp32 tables")
+    cos2, sin2 = cos.reshape(-1, d // 2).contiguous(), sin.reshape(-1, d // 2).contiguous()
+    pos = positions if positions.dtype == torch.int32 else positions.to(torch.int32)
+    pos = pos.contiguous()
+    if pos.numel() != T:
+        raise ValueError("linear_rope_qkv_rmsnorm: positions and x disagree on the token count")
+    q = torch.empty((T, hq, d), dtype=x.dtype, device=x.device)
+    k = torch.empty((T, hkv, d), dtype=x.dtype, device=x.device)
+    v = torch.empty((T, hkv, d), dtype=x.dtype, device=x.device)
+    rc = _native.lib().pkv_linear_rope_qkv_rmsnorm(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), x2.data_ptr(), norm_weight.data_ptr(),
+        float(eps), w_qkv.data_ptr(), _native.ptr(b_qkv), T, x2.shape[1], _x_stride(x2),
+        pos.data_ptr(), cos2.data_ptr(), sin2.data_ptr(), cos2.shape[0], hq, hkv, d,
+        _native.dtype_code(x.dtype), None, _native.stream_ptr(x.device))
+    _native.check(rc, "linear_rope_qkv_rmsnorm")
+    return q, k, v
+
+
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Index of the largest logit of every row of [rows, vocab] logits as
     int64 [rows] (pkv_argmax_rows; the framework's argmax result: first

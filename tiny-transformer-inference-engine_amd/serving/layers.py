@@ -121,6 +121,14 @@ class SwiGLU(nn.Module):
             return fused_ops.linear(h, self.down_proj.weight, self.down_proj.bias)
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
+    def forward_residual_(self, x, norm):
+        """x += forward(norm(x)) in place on a ROCm device, the norm taken in
+        the gate/up projection's prologue and the add in down_proj's
+        epilogue (the same rounded values as the separate ops). Returns x."""
+        w, b = self._gate_up.get()
+        h = fused_ops.linear_swiglu_rmsnorm(x, norm.weight, norm.eps, w, b)
+        return fused_ops.linear_residual_(x, h, self.down_proj.weight, self.down_proj.bias)
+
 
 class TokenEmbedding(nn.Module):
     def __init__(self, vocab_size, embed_dim):

@@ -66,28 +66,26 @@ class PagedTransformer(nn.Module):
     def forward_step(self, input_ids, pool, meta):
         """forward_batch with pre-packed metadata (PagedBatchMeta).
 
-        On a ROCm device every residual add runs inside the norm that
-        follows it (fused_ops.add_rms_norm_: x += delta, then normalise x),
-        so a layer is: norm, qkv GEMM, RoPE, append + attention, out GEMM,
-        add + norm, gate/up GEMM, SwiGLU gate, down GEMM. The arithmetic is
-        that of PagedBlock.forward_meta: each sum is rounded to the model
-        dtype before it is normalised or carried on."""
+        On a ROCm device every norm runs in the prologue of the projection
+        that consumes it and every residual add in the epilogue of the
+        projection that produces it, so a layer is four projection kernels
+        and one attention call: norm + qkv GEMM + RoPE, append + attention,
+        out GEMM + add, norm + gate/up GEMM + SwiGLU gate, down GEMM + add.
+        The arithmetic is that of PagedBlock.forward_meta: each sum is
+        rounded to the model dtype before it is normalised or carried on."""
         x = self.embedding(input_ids)
         last = meta.query_start_loc[1:].long() - 1
         if not x.is_cuda:
             for layer in self.layers:
                 x = layer.forward_meta(x, pool, meta)
             return self.lm_head(self.final_norm(x.index_select(0, last)))
-        norms = [layer.attn_norm for layer in self.layers] + [self.final_norm]
-        h = norms[0](x)
-        for i, layer in enumerate(self.layers):
-            a = layer.attn.forward_meta(h, pool, layer.layer_idx, meta)
-            h = fused_ops.add_rms_norm_(x, a, layer.mlp_norm.weight, layer.mlp_norm.eps)
-            m = layer.mlp(h)
-            h = fused_ops.add_rms_norm_(x, m, norms[i + 1].weight, norms[i + 1].eps)
+        x = x.contiguous()
+        for layer in self.layers:
+            layer.attn.forward_meta_residual_(x, layer.attn_norm, pool, layer.layer_idx, meta)
+            layer.mlp.forward_residual_(x, layer.mlp_norm)
         if not meta.is_decode:
-            h = h.index_select(0, last)
-        return self.lm_head(h)
+            x = x.index_select(0, last)
+        return self.lm_head(self.final_norm(x))
 
 
 def load_paged_model(ckpt_path, device):

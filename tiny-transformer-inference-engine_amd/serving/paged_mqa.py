@@ -101,3 +101,18 @@ class MQA_Paged(nn.Module):
         # append + attention in one library call (fused on the decode kernels)
         out = paged_attention_append_meta(q, k, v, pool, layer_idx, meta)
         return fused_ops.linear(out.view(T, d_model), self.out.weight, self.out.bias)
+
+    def forward_meta_residual_(self, x, norm, pool, layer_idx, meta: PagedBatchMeta):
+        """x += forward_meta(norm(x), ...) in place, with the norm taken in
+        the qkv projection's prologue and the residual add in the out
+        projection's epilogue (the same rounded values as the separate
+        norm, layer and add). Returns x."""
+        T, d_model = x.shape
+        w, b = self._qkv.get()
+        cos, sin = self.rope._tables_fp32()
+        q, k, v = fused_ops.linear_rope_qkv_rmsnorm(x, norm.weight, norm.eps, w, b,
+                                                    meta.positions, cos, sin, self.num_heads,
+                                                    self.num_kv_heads, self.headdim)
+        out = paged_attention_append_meta(q, k, v, pool, layer_idx, meta)
+        return fused_ops.linear_residual_(x, out.view(T, d_model), self.out.weight,
+                                          self.out.bias)
