@@ -156,13 +156,17 @@ def test_records_of_previous_call_do_not_leak(pt):
 
 
 def _counters():
-    """The dynamic persistent kernel's draw and arrival counters (first
-    8 KiB of the library workspace on this device)."""
+    """The persistent kernels' counters in the library workspace on this
+    device: the dynamic kernel's draw and arrival counters (first 8 KiB) and
+    the static kernel's per-sequence arrival counters (the last int of each
+    16-byte record after them)."""
     buf = _native.WORKSPACE._bufs[torch.cuda.current_device()]
-    return buf[: 8 * 1024].view(torch.int32)
+    recs = buf[8 * 1024: 256 * 1024].view(torch.int32).view(-1, 4)
+    return torch.cat([buf[: 8 * 1024].view(torch.int32), recs[:, 3]])
 
 
-def test_cut_sequences_alternating_inputs_and_counters_reset():
+@pytest.mark.parametrize("pt", [STATIC, DYN])
+def test_cut_sequences_alternating_inputs_and_counters_reset(pt):
     """Pieces of long sequences are merged inside the kernel by the last
     workgroup to arrive, from partials other workgroups (on other XCDs)
     stored just before. Two problems with the same lengths and tables but different
@@ -181,7 +185,7 @@ def test_cut_sequences_alternating_inputs_and_counters_reset():
         name, p = ("a", pa) if i % 2 == 0 else ("b", pb)
         lse = torch.empty(len(lens), g, device=DEV)
         out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, lse=lse,
-                               part_tokens=DYN)
+                               part_tokens=pt)
         torch.cuda.synchronize()
         check(out, lse, *refs[name], f"call {i} ({name})")
         assert int(_counters().abs().sum()) == 0, f"call {i}: arrival counters not reset"
@@ -209,10 +213,11 @@ def test_persistent_random_length_mixes(seed):
                                  seed=200 + seed)
     seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
     eo, el = oracle(p, seq_lens)
-    for rep in range(2):
+    for rep in range(4):
+        pt = DYN if rep % 2 == 0 else STATIC
         lse = torch.empty(n, g, device=DEV)
         out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
-                               part_tokens=DYN)
+                               part_tokens=pt)
         torch.cuda.synchronize()
-        check(out, lse, eo, el, f"mix seed {seed} rep {rep}")
+        check(out, lse, eo, el, f"mix seed {seed} rep {rep} part_tokens {pt}")
         assert int(_counters().abs().sum()) == 0, "arrival counters not reset"

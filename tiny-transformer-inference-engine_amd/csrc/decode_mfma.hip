@@ -171,51 +171,49 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
 
   T* __restrict__ out = static_cast<T*>(a.out);
   const int64_t unit = (int64_t)blockIdx.x * a.parts_max + part;
-  for (int idx = threadIdx.x; idx < G * D / 4; idx += kBlock) {
-    const int head = idx / (D / 4);
-    const int d0 = (idx - head * (D / 4)) * 4;
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, ml_lds[ww][head][0]);
-    float L = 0.f;
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) {
-        const float wt = exp2f(ml_lds[ww][head][0] - M);
-        L += ml_lds[ww][head][1] * wt;
-        acc += wt * *reinterpret_cast<const floatx4*>(ob + (ww * G + head) * OPITCH + d0);
-      }
-    }
-    const int64_t qrow = qrow0 + head;
+  using Combine = WaveCombine<G, D, kWaves, kBlock>;
+  {
+    Combine cb;
+    cb.run(ob, ml_lds, threadIdx.x);
+    const int64_t qrow = qrow0 + cb.head;
     if (g.nparts == 1) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      T* dst = out + qrow * D + d0;
-      dst[0] = (T)(acc[0] * inv);
-      dst[1] = (T)(acc[1] * inv);
-      dst[2] = (T)(acc[2] * inv);
-      dst[3] = (T)(acc[3] * inv);
-      if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
-    } else if (a.merge_ctr) {
-      // written through to memory: the merging workgroup may sit on another
-      // XCD
-      uint64_t b0, b1;
-      __builtin_memcpy(&b0, &acc, 8);
-      __builtin_memcpy(&b1, reinterpret_cast<const char*>(&acc) + 8, 8);
-      float* po = a.ws_o + (unit * G + head) * D + d0;
-      st_agent64(po, b0);
-      st_agent64(po + 2, b1);
-      if (d0 == 0) {
-        const float2 ml = make_float2(M, L);
-        uint64_t bm;
-        __builtin_memcpy(&bm, &ml, 8);
-        st_agent64(a.ws_ml + (unit * G + head) * 2, bm);
+#pragma unroll
+      for (int q = 0; q < Combine::NQ; ++q) {
+        T* dst = out + qrow * D + cb.col(q);
+        dst[0] = (T)(cb.acc[q][0] * cb.inv);
+        dst[1] = (T)(cb.acc[q][1] * cb.inv);
+        dst[2] = (T)(cb.acc[q][2] * cb.inv);
+        dst[3] = (T)(cb.acc[q][3] * cb.inv);
       }
+      if (cb.cq == 0 && a.lse) a.lse[qrow] = cb.L > 0.f ? (cb.M + log2f(cb.L)) * kLn2f : INFINITY;
     } else {
-      *reinterpret_cast<floatx4*>(a.ws_o + (unit * G + head) * D + d0) = acc;
-      if (d0 == 0) {
-        a.ws_ml[(unit * G + head) * 2 + 0] = M;
-        a.ws_ml[(unit * G + head) * 2 + 1] = L;
+      const int64_t prow = unit * G + cb.head;
+      if (a.merge_ctr) {
+        // written through to memory: the merging workgroup may sit on
+        // another XCD
+#pragma unroll
+        for (int q = 0; q < Combine::NQ; ++q) {
+          uint64_t b0, b1;
+          __builtin_memcpy(&b0, &cb.acc[q], 8);
+          __builtin_memcpy(&b1, reinterpret_cast<const char*>(&cb.acc[q]) + 8, 8);
+          float* po = a.ws_o + prow * D + cb.col(q);
+          st_agent64(po, b0);
+          st_agent64(po + 2, b1);
+        }
+        if (cb.cq == 0) {
+          const float2 ml = make_float2(cb.M, cb.L);
+          uint64_t bm;
+          __builtin_memcpy(&bm, &ml, 8);
+          st_agent64(a.ws_ml + prow * 2, bm);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < Combine::NQ; ++q)
+          *reinterpret_cast<floatx4*>(a.ws_o + prow * D + cb.col(q)) = cb.acc[q];
+        if (cb.cq == 0) {
+          a.ws_ml[prow * 2 + 0] = cb.M;
+          a.ws_ml[prow * 2 + 1] = cb.L;
+        }
       }
     }
   }
@@ -223,8 +221,9 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
 
   // ---- in-kernel split-K merge: once its partial stores have completed,
   // each partition counts itself in; the one that brings the count to
-  // nparts merges every partition (loads issued in batches of 8 before any
-  // is consumed, as merge_kernel does), writes the rows and resets the
+  // nparts merges every partition (each thread one head and the columns of
+  // the wavefront combination above; loads issued in batches of 8
+  // partitions before any is consumed), writes the rows and resets the
   // counter for the next call. No workgroup waits for another.
   __shared__ int s_last;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -239,40 +238,47 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   if (!s_last) return;
   const int64_t unit0 = (int64_t)blockIdx.x * a.parts_max;
   constexpr int kMB = 8;
-  for (int idx = threadIdx.x; idx < G * D / 4; idx += kBlock) {
-    const int head = idx / (D / 4);
-    const int d0 = (idx - head * (D / 4)) * 4;
-    float M = -INFINITY, L = 0.f;
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int p0 = 0; p0 < g.nparts; p0 += kMB) {
-      float2 ml[kMB];
-      floatx4 oo[kMB];
+  constexpr int NQ = Combine::NQ;
+  const int head = threadIdx.x / Combine::TPH;
+  const int cq = threadIdx.x - head * Combine::TPH;
+  float M = -INFINITY, L = 0.f;
+  floatx4 acc[NQ];
 #pragma unroll
-      for (int j = 0; j < kMB; ++j) {
-        const int64_t row = (unit0 + min(p0 + j, g.nparts - 1)) * G + head;
-        ml[j] = *reinterpret_cast<const float2*>(a.ws_ml + row * 2);
-        oo[j] = *reinterpret_cast<const floatx4*>(a.ws_o + row * D + d0);
-      }
+  for (int q = 0; q < NQ; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int p0 = 0; p0 < g.nparts; p0 += kMB) {
+    float2 ml[kMB];
+    floatx4 oo[kMB][NQ];
 #pragma unroll
-      for (int j = 0; j < kMB; ++j) {
-        if (p0 + j >= g.nparts || ml[j].x == -INFINITY) continue;
-        const float Mn = fmaxf(M, ml[j].x);
-        const float sa = exp2f(M - Mn);
-        const float sb = exp2f(ml[j].x - Mn);
-        L = L * sa + ml[j].y * sb;
-        acc = acc * sa + oo[j] * sb;
-        M = Mn;
-      }
+    for (int j = 0; j < kMB; ++j) {
+      const int64_t row = (unit0 + min(p0 + j, g.nparts - 1)) * G + head;
+      ml[j] = *reinterpret_cast<const float2*>(a.ws_ml + row * 2);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+        oo[j][q] = *reinterpret_cast<const floatx4*>(a.ws_o + row * D + 4 * (cq + Combine::TPH * q));
     }
-    const int64_t qrow = qrow0 + head;
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    T* dst = out + qrow * D + d0;
-    dst[0] = (T)(acc[0] * inv);
-    dst[1] = (T)(acc[1] * inv);
-    dst[2] = (T)(acc[2] * inv);
-    dst[3] = (T)(acc[3] * inv);
-    if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      if (p0 + j >= g.nparts || ml[j].x == -INFINITY) continue;
+      const float Mn = fmaxf(M, ml[j].x);
+      const float sa = exp2f(M - Mn);
+      const float sb = exp2f(ml[j].x - Mn);
+      L = L * sa + ml[j].y * sb;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) acc[q] = acc[q] * sa + oo[j][q] * sb;
+      M = Mn;
+    }
   }
+  const int64_t qrow = qrow0 + head;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    T* dst = out + qrow * D + 4 * (cq + Combine::TPH * q);
+    dst[0] = (T)(acc[q][0] * inv);
+    dst[1] = (T)(acc[q][1] * inv);
+    dst[2] = (T)(acc[q][2] * inv);
+    dst[3] = (T)(acc[q][3] * inv);
+  }
+  if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
 // <T, D, NT, PF, OCC, OFF64, APP>: two wavefronts per SIMD

@@ -123,6 +123,83 @@ __device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
   return __builtin_amdgcn_readfirstlane(total);
 }
 
+// Cut sequences are merged inside the launch by the workgroup that stores
+// the last of their partials (true), or by sk_merge_kernel launched after it
+// (false).
+constexpr bool kInKernelMerge = true;
+
+__device__ __forceinline__ uint64_t ld_agent64(const void* p) {
+  return __hip_atomic_load(static_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Partial slot of contributor ww of a sequence cut over [w_first, w_last]:
+// the sequence is the first segment of every contributor but w_first, whose
+// slot is 2 w_first + r_slot (r_slot = 1 when its share starts with an
+// earlier sequence).
+__device__ __forceinline__ int64_t cut_slot(int ww, int w_first, int r_slot) {
+  return ww == w_first ? 2 * (int64_t)ww + r_slot : 2 * (int64_t)ww;
+}
+
+// Combination of every partial of a cut sequence, in contributor order (so
+// the result does not depend on which contributor merges): thread tid owns
+// head tid / TPH and the float4 columns cq + TPH q, the (max, sum) pair of
+// its head is read once per contributor, and every load of a batch of kMB
+// contributors is issued before any is consumed. The arithmetic is
+// sk_merge_kernel's. Loads are device-coherent (they bypass this XCD's L2:
+// the partials were written through from other XCDs during this launch).
+template <typename T, int G, int D>
+__device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, int w_first,
+                                          int w_last, int r_slot, int64_t qrow0, int tid) {
+  constexpr int TPH = kBlock / G;
+  constexpr int NQ = D / (4 * TPH);
+  constexpr int kMB = 4;
+  const int head = tid / TPH;
+  const int cq = tid - head * TPH;
+  float M = -INFINITY, L = 0.f;
+  floatx4 acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int wb = w_first; wb <= w_last; wb += kMB) {
+    uint64_t mlr[kMB], oor[kMB][NQ];
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      const int64_t row = cut_slot(min(wb + j, w_last), w_first, r_slot) * G + head;
+      mlr[j] = ld_agent64(k.part_ml + row * 2);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) oor[j][q] = ld_agent64(k.part_o + row * D + 4 * (cq + TPH * q));
+    }
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) {
+      float2 ml;
+      __builtin_memcpy(&ml, &mlr[j], 8);
+      if (wb + j > w_last || ml.x == -INFINITY) continue;
+      const float Mn = fmaxf(M, ml.x);
+      const float sa = exp2f(M - Mn);
+      const float wl = ml.y * exp2f(ml.x - Mn);  // this partial's weight
+      L = L * sa + wl;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        half4 oo;
+        __builtin_memcpy(&oo, &oor[j][q], 8);
+        acc[q] = acc[q] * sa + floatx4{(float)oo[0], (float)oo[1], (float)oo[2], (float)oo[3]} * wl;
+      }
+      M = Mn;
+    }
+  }
+  const int64_t qrow = qrow0 + head;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    T* dst = static_cast<T*>(a.out) + qrow * D + 4 * (cq + TPH * q);
+    dst[0] = (T)(acc[q][0] * inv);
+    dst[1] = (T)(acc[q][1] * inv);
+    dst[2] = (T)(acc[q][2] * inv);
+    dst[3] = (T)(acc[q][3] * inv);
+  }
+  if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
+}
+
 template <typename T, int D, int NT, int PF, bool OFF64>
 __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs k) {
   using Geo = ChunkGeo<D>;
@@ -138,7 +215,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   __shared__ float ml_lds[kWaves][G][2];
   __shared__ int tbl[kTblCap];
   __shared__ int scan_sh[kBlock];
-  __shared__ int s_v0, s_g0;
+  __shared__ int s_v0, s_g0, s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -237,6 +314,10 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     const int kv_len = dsc.kv_len;
     const int c0 = max(0, start - (g0 + K));
     const int c1 = min(n, end - (g0 + K));
+    // a share shorter than seg_cost can lie entirely in v's overhead units:
+    // it owns none of v's chunks (nor any later ones), so it is no
+    // contributor and has nothing to do
+    if (c1 <= c0) break;
     const bool whole = c0 == 0 && c1 == n;
     const int s = v / a.hkv;
     const int kvh = v - s * a.hkv;
@@ -326,45 +407,75 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     }
     __syncthreads();
     const int slot = 2 * wg + (first ? 0 : 1);
-    for (int idx = tid; idx < G * D / 4; idx += kBlock) {
-      const int head = idx / (D / 4);
-      const int d0 = (idx - head * (D / 4)) * 4;
-      float M = -INFINITY;
-#pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, ml_lds[ww][head][0]);
-      float L = 0.f;
-      floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) {
-          const float wt = exp2f(ml_lds[ww][head][0] - M);
-          L += ml_lds[ww][head][1] * wt;
-          acc += wt * *reinterpret_cast<const floatx4*>(ob + (ww * G + head) * OPITCH + d0);
-        }
-      }
+    {
+      WaveCombine<G, D, kWaves, kBlock> cb;
+      cb.run(ob, ml_lds, tid);
+      const float inv = cb.inv;
       if (whole) {
-        const int64_t qrow = qrow0 + head;
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        T* dst = out + qrow * D + d0;
-        dst[0] = (T)(acc[0] * inv);
-        dst[1] = (T)(acc[1] * inv);
-        dst[2] = (T)(acc[2] * inv);
-        dst[3] = (T)(acc[3] * inv);
-        if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
+        const int64_t qrow = qrow0 + cb.head;
+#pragma unroll
+        for (int q = 0; q < cb.NQ; ++q) {
+          T* dst = out + qrow * D + cb.col(q);
+          dst[0] = (T)(cb.acc[q][0] * inv);
+          dst[1] = (T)(cb.acc[q][1] * inv);
+          dst[2] = (T)(cb.acc[q][2] * inv);
+          dst[3] = (T)(cb.acc[q][3] * inv);
+        }
+        if (cb.cq == 0 && a.lse)
+          a.lse[qrow] = cb.L > 0.f ? (cb.M + log2f(cb.L)) * kLn2f : INFINITY;
       } else {
         // normalised by its own sum (a weighted mean of value rows, so its
         // range is theirs) and rounded to fp16: half the partial traffic
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        *reinterpret_cast<half4*>(k.part_o + ((int64_t)slot * G + head) * D + d0) =
-            half4{(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
-                  (_Float16)(acc[3] * inv)};
-        if (d0 == 0)
-          *reinterpret_cast<float2*>(k.part_ml + ((int64_t)slot * G + head) * 2) =
-              make_float2(M, L);
+        const int64_t prow = (int64_t)slot * G + cb.head;
+#pragma unroll
+        for (int q = 0; q < cb.NQ; ++q) {
+          const half4 h = half4{(_Float16)(cb.acc[q][0] * inv), (_Float16)(cb.acc[q][1] * inv),
+                                (_Float16)(cb.acc[q][2] * inv), (_Float16)(cb.acc[q][3] * inv)};
+          if constexpr (kInKernelMerge) {
+            // written through: the merging workgroup may sit on another XCD
+            uint64_t b;
+            __builtin_memcpy(&b, &h, 8);
+            st_agent64(k.part_o + prow * D + cb.col(q), b);
+          } else {
+            *reinterpret_cast<half4*>(k.part_o + prow * D + cb.col(q)) = h;
+          }
+        }
+        if (cb.cq == 0) {
+          const float2 ml = make_float2(cb.M, cb.L);
+          if constexpr (kInKernelMerge) {
+            uint64_t b;
+            __builtin_memcpy(&b, &ml, 8);
+            st_agent64(k.part_ml + prow * 2, b);
+          } else {
+            *reinterpret_cast<float2*>(k.part_ml + prow * 2) = ml;
+          }
+        }
       }
     }
 
-    if (c0 == 0 && tid == 0) {
+    if constexpr (kInKernelMerge) {
+      if (!whole) {
+        // once this workgroup's partial stores have completed, it counts
+        // itself in on the sequence's arrival counter (the last int of its
+        // record); the contributor that brings the count to the number of
+        // contributors merges every partial and puts the counter back to
+        // zero for the next call. No workgroup waits for another.
+        const int w_first = share_owner(g0 + K, C, W);
+        const int w_last = share_owner(g0 + K + n - 1, C, W);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+          int* ctr = reinterpret_cast<int*>(k.recs + v) + 3;
+          const int old = fetch_add_agent(ctr, 1);
+          s_last = old == w_last - w_first;
+          if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (s_last)
+          merge_cut<T, G, D>(a, k, w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0,
+                             qrow0, tid);
+      }
+    } else if (c0 == 0 && tid == 0) {
       // contributors of this sequence, for the merge kernel
       const int w_first = share_owner(g0 + K, C, W);
       const int w_last = share_owner(g0 + K + n - 1, C, W);
@@ -448,7 +559,7 @@ int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
   hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64>), dim3(k.n_wg), dim3(kBlock), 0,
                      stream, a, k);
   int rc = check_launch("decode_sk_kernel");
-  if (rc != PKV_OK) return rc;
+  if (rc != PKV_OK || kInKernelMerge) return rc;
   constexpr int G = 16 * NT;
   const dim3 mgrid(a.n_seq * a.hkv, (G * D / 4 + kMergeBlock - 1) / kMergeBlock);
   hipLaunchKernelGGL((sk_merge_kernel<T, G, D>), mgrid, dim3(kMergeBlock), 0, stream, a, k);

@@ -403,6 +403,51 @@ __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
                                        bad_block, nr);
 }
 
+// Combination of the NW wavefronts' online-softmax states of one
+// (sequence, kv head) after they are staged in LDS: ob = [NW][G][D + 4]
+// floats (O of each wavefront), ml = [NW][G] (m, l). Thread tid of BLOCK
+// owns head tid / TPH and the float4 columns cq + TPH q (q < NQ), so the
+// softmax weights of the wavefronts, the sum and its reciprocal are taken
+// once per head and thread rather than once per output column, and
+// consecutive threads read and write consecutive columns.
+template <int G, int D, int NW, int BLOCK>
+struct WaveCombine {
+  static constexpr int TPH = BLOCK / G;        // threads per head
+  static constexpr int NQ = D / (4 * TPH);     // float4 columns per thread
+  static constexpr int OPITCH = D + 4;
+  static_assert(BLOCK % G == 0 && NQ >= 1 && D % (4 * TPH) == 0, "block / head split");
+  int head, cq;
+  float M, L, inv;  // running max (base 2), sum, 1 / sum (0 when the sum is 0)
+  floatx4 acc[NQ];  // unnormalised output columns
+
+  __device__ __forceinline__ int col(int q) const { return 4 * (cq + TPH * q); }
+
+  __device__ __forceinline__ void run(const float* ob, const float (*ml)[G][2], int tid) {
+    head = tid / TPH;
+    cq = tid - head * TPH;
+    M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, ml[ww][head][0]);
+    L = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
+      float wt[NW];
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        wt[ww] = exp2f(ml[ww][head][0] - M);
+        L += ml[ww][head][1] * wt[ww];
+      }
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          acc[q] += wt[ww] * *reinterpret_cast<const floatx4*>(ob + (ww * G + head) * OPITCH + col(q));
+    }
+    inv = L > 0.f ? 1.f / L : 0.f;
+  }
+};
+
 // Fused append of one sequence's query-token row. load_new_row /
 // put_new_row: threads [0, 2 CPR) of the workgroup copy their 16-byte piece
 // of the K / V row `tok` (kv head `kvh`) into the LDS row buffer (the
