@@ -460,8 +460,9 @@ def main():
                        "replayed from one HIP graph",
         "decode_tok_s_eager": None if model is None else round(N_MODEL / model["eager_step_sec"], 1),
         "roofline": {
-            "kernel": "paged MQA decode attention, cfg4, one layer: decode_mfma_kernel + "
-                      "split-K merge_kernel (one launch pair, timed together)",
+            "kernel": "paged MQA decode attention, cfg4, one layer: decode_mfma_kernel "
+                      "(split-K partitions merged in-kernel by the last one to finish; one "
+                      "launch)",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
