@@ -54,6 +54,9 @@
  *                                                    serving/paged_model.py:26-27,
  *                                                    models/rmsnorm.py:12-18, serving/paged_mqa.py:76-85
  *   pkv_argmax_rows       greedy token choice: logits.argmax per sequence
+ *   pkv_sample_rows       sample(): temperature, top-k, top-p, one draw per
+ *                         row (sampling.py:94-137; the top-k step of
+ *                         kernels/cuda-kSAMPLING/ksampling_kernel.cu:61-185)
  *                                                    serving/generation.py:77,88,132,142;
  *                         greedy()                   sampling.py:5-137
  */
@@ -97,6 +100,10 @@ extern "C" {
 #define PKV_STATUS_SHORT_TABLE 4 /* append: position beyond the table      */
 #define PKV_STATUS_BAD_QLOC 8    /* attention: query range outside [0, T)  */
 #define PKV_STATUS_BAD_POS 16    /* rope: position outside [0, max_pos)    */
+#define PKV_STATUS_NONFINITE 32  /* sampling: a logit is NaN or infinite    */
+#define PKV_STATUS_BAD_DISTRIBUTION 64 /* sampling: logit / temperature overflowed */
+#define PKV_STATUS_SAMPLE_OVERFLOW 128 /* sampling: too many ties at the top-k
+                                          threshold for the kernel (id -1)    */
 
 /* Library version (PKV_VERSION). */
 int pkv_version(void);
@@ -364,6 +371,26 @@ int pkv_linear_rope_qkv_rmsnorm(void* q_out, void* k_out, void* v_out, const voi
  */
 int pkv_argmax_rows(int64_t* ids, const void* logits, int64_t rows, int64_t vocab,
                     int64_t row_stride, int dtype, void* stream);
+
+/*
+ * Sampling step of the scheduler (sampling.py:94-137, sample()): per row of
+ * logits [rows, vocab] (row_stride elements apart, fp32 / bf16 / fp16),
+ * y = logits / temperature in fp32; keep every y >= the top_k-th largest
+ * (ties kept, as apply_top_k); sort the kept values descending (ties by
+ * ascending index) and keep the prefix whose softmax mass before each token
+ * is at most top_p (the first always, as apply_top_p); renormalise; ids[r]
+ * (int64) = the first kept index, in ascending vocabulary order, whose
+ * cumulative probability exceeds uniforms[r] * total (uniforms: fp32 in
+ * [0, 1), one per row, the caller's random numbers). 1 <= top_k <= 64
+ * (PKV_ERR_UNSUPPORTED otherwise), 0 < top_p <= 1, temperature finite > 0.
+ * Status bits (ids[r] = -1 for the row): PKV_STATUS_NONFINITE (a NaN or
+ * infinite logit), PKV_STATUS_BAD_DISTRIBUTION (y overflowed),
+ * PKV_STATUS_SAMPLE_OVERFLOW (more than 1024 values tie or crowd at the
+ * threshold's neighbourhood; sample such a row another way).
+ */
+int pkv_sample_rows(int64_t* ids, const void* logits, int64_t rows, int64_t vocab,
+                    int64_t row_stride, float temperature, int top_k, float top_p,
+                    const float* uniforms, int dtype, int* status, void* stream);
 
 #ifdef __cplusplus
 }

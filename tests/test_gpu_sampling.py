@@ -4,11 +4,21 @@ the framework's NaN order. Vocabulary sizes with unaligned rows (50257:
 rows start off a 16-byte boundary), tiny and large rows, strided rows,
 planted ties inside one 16-byte vector, across threads and across
 wavefronts, NaN rows, all -inf rows; fp32 / fp16 / bf16. Also the greedy
-decode-step helpers that use it (sampling.greedy)."""
+decode-step helpers that use it (sampling.greedy).
+
+The fused top-k / top-p sampling kernel (pkv_sample_rows) against the
+float64 restatement at the same uniforms (oracle/sampling_ref.py): kept set
+and drawn token, fp32 / bf16 / fp16, vocabularies of 37 to 50257, top_k 1
+to 64, ties at the threshold, strided rows, the draw frequencies over a
+grid of uniforms, the reference's errors and the fallback when the kernel
+declines a call."""
+import numpy as np
 import pytest
 import torch
 
-from serving import fused_ops, sampling
+from oracle import sampling_ref as sref
+from serving import _native, fused_ops, sampling
+from serving import sampling as smp
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -61,3 +71,104 @@ def test_greedy_helper_uses_kernel():
     out = sampling.greedy(logits)
     assert out.shape == (16, 1) and out.dtype == torch.long
     assert torch.equal(out.cpu(), logits.cpu().argmax(-1, keepdim=True))
+
+
+# ---- fused top-k / top-p sampling (pkv_sample_rows) against the float64
+# restatement (oracle/sampling_ref.py) at the same uniforms; a row whose
+# uniform lies within 1e-5 of a bucket edge (fp32 vs fp64 sums) is skipped,
+# and most rows must be checked.
+
+
+def _check_rows(logits, temperature, top_k, top_p, seed, min_checked=0.9):
+    rows = logits.shape[0]
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    u = torch.rand(rows, generator=g, device=DEV)
+    ids, status = fused_ops.sample_rows(logits, temperature, top_k, top_p, u)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    x = logits.float().cpu().numpy().astype(np.float64)
+    y32 = (logits.float() / temperature).cpu().numpy().astype(np.float64)
+    got = ids.cpu().numpy()
+    checked = 0
+    for r in range(rows):
+        keep, probs = sref.sample_probs(y32[r], 1.0, top_k, top_p)
+        # a top-p boundary within rounding (equal masses from ties) may keep
+        # one token more or less in fp32 than in fp64: such rows are skipped
+        kk = sref.top_k_keep(y32[r], top_k)
+        kidx = np.nonzero(kk)[0]
+        order = kidx[np.lexsort((kidx, -y32[r][kidx]))]
+        e = np.exp(y32[r][order] - y32[r][order[0]])
+        near_p = top_p < 1.0 and np.min(np.abs(np.cumsum(e / e.sum()) - top_p)) < 1e-5
+        if near_p:
+            continue
+        assert keep[got[r]], f"row {r}: token {got[r]} outside the top-k/top-p set"
+        want, margin = sref.pick(probs, float(u[r]))
+        if margin > 1e-5:
+            assert got[r] == want, f"row {r}: kernel {got[r]} oracle {want}"
+            checked += 1
+    assert checked >= min_checked * rows, f"only {checked} of {rows} rows checked"
+    del x
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,vocab,top_k,top_p,temp", [
+    (128, 50257, 32, 0.9, 1.0),
+    (64, 50257, 64, 1.0, 0.7),
+    (33, 1000, 5, 0.5, 1.3),
+    (7, 37, 64, 0.95, 1.0),
+    (16, 4096, 1, 1.0, 1.0),
+])
+def test_sample_rows_vs_oracle(dtype, rows, vocab, top_k, top_p, temp):
+    print(f"[sample_rows] {dtype} rows={rows} vocab={vocab} k={top_k} p={top_p} t={temp}",
+          flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows * vocab)
+    logits = (3 * torch.randn(rows, vocab, generator=g, device=DEV)).to(dtype)
+    _check_rows(logits, temp, top_k, top_p, seed=rows + top_k)
+
+
+def test_sample_rows_ties_and_strided_rows():
+    # bf16 logits on a coarse grid: many values tie at the top-k threshold
+    g = torch.Generator(device=DEV).manual_seed(5)
+    base = torch.randint(0, 12, (40, 3000), generator=g, device=DEV).float() / 4
+    logits = base.to(torch.bfloat16)
+    _check_rows(logits, 1.0, 16, 0.77, seed=6, min_checked=0.6)
+    wide = torch.zeros(40, 3200, dtype=torch.bfloat16, device=DEV)
+    wide[:, 100:3100] = logits
+    _check_rows(wide[:, 100:3100], 1.0, 16, 0.77, seed=6, min_checked=0.6)
+
+
+def test_sample_top_k_1_is_argmax_and_distribution_matches():
+    g = torch.Generator(device=DEV).manual_seed(9)
+    logits = torch.randn(256, 5000, generator=g, device=DEV)
+    u = torch.rand(256, generator=g, device=DEV)
+    ids, st = fused_ops.sample_rows(logits, 1.0, 1, 1.0, u)
+    assert torch.equal(ids, torch.argmax(logits, dim=-1))
+    # one row drawn at a grid of uniforms: the frequencies are the probabilities
+    row = torch.tensor([[2.0, 1.0, 0.5, 0.0, -1.0] + [-30.0] * 59], device=DEV)
+    n = 4096
+    us = (torch.arange(n, device=DEV, dtype=torch.float32) + 0.5) / n
+    ids, st = fused_ops.sample_rows(row.expand(n, -1).contiguous(), 1.0, 4, 1.0, us)
+    freq = torch.bincount(ids, minlength=64).float().cpu().numpy() / n
+    _, probs = sref.sample_probs(row[0].cpu().numpy().astype(np.float64), 1.0, 4, 1.0)
+    assert np.allclose(freq, probs, atol=2e-3)
+
+
+def test_sample_errors_and_overflow_fallback():
+    with pytest.raises(ValueError, match="NaN or infinity"):
+        smp.sample(torch.tensor([[0.0, float("nan")]], device=DEV), top_k=2)
+    # every logit equal: all 5000 values reach the threshold -> the kernel
+    # declines the call and sample() draws with the framework path
+    flat = torch.zeros(3, 5000, device=DEV)
+    u = torch.rand(3, device=DEV)
+    ids, st = fused_ops.sample_rows(flat, 1.0, 32, 0.9, u)
+    assert int(st.item()) & _native.PKV_STATUS_SAMPLE_OVERFLOW
+    tok = smp.sample(flat, temperature=1.0, top_k=32, top_p=0.9)
+    assert tok.shape == (3, 1) and bool(((tok >= 0) & (tok < 5000)).all())
+    # the kernel path of sample(): tokens inside the kept set
+    g = torch.Generator(device=DEV).manual_seed(11)
+    logits = torch.randn(64, 50257, generator=g, device=DEV).bfloat16()
+    tok = smp.sample(logits, temperature=1.0, top_k=32, top_p=0.9).squeeze(-1).cpu().numpy()
+    y = logits.float().cpu().numpy().astype(np.float64)
+    for r in range(64):
+        keep, _ = sref.sample_probs(y[r], 1.0, 32, 0.9)
+        assert keep[tok[r]]

@@ -27,6 +27,9 @@ PKV_STATUS_BAD_BLOCK = 2
 PKV_STATUS_SHORT_TABLE = 4
 PKV_STATUS_BAD_QLOC = 8
 PKV_STATUS_BAD_POS = 16
+PKV_STATUS_NONFINITE = 32
+PKV_STATUS_BAD_DISTRIBUTION = 64
+PKV_STATUS_SAMPLE_OVERFLOW = 128
 # part_tokens values selecting a persistent decode kernel: the one the
 # library prefers, the one with static equal shares, or the dynamically
 # scheduled one (largest-first work items drawn from a counter; up to 1024
@@ -89,6 +92,8 @@ _SIGNATURES = {
                                      _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _c_vp, _c_vp], _c_int),
     "pkv_argmax_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp], _c_int),
+    "pkv_sample_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_float,
+                         _c_vp, _c_int, _c_vp, _c_vp], _c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -350,6 +350,31 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     return out
 
 
+def sample_rows(logits: torch.Tensor, temperature: float, top_k: int, top_p: float,
+                uniforms: torch.Tensor):
+    """One draw per row of [rows, vocab] logits with temperature, top-k
+    (1..64, ties at the threshold kept) and top-p, by inverse CDF at the
+    row's uniform in [0, 1) (pkv_sample_rows). Returns (ids int64 [rows],
+    status int32 [1]: PKV_STATUS_* bits; a flagged row's id is -1)."""
+    _native.require_device(logits, uniforms, what="sample_rows")
+    if logits.dim() != 2:
+        raise ValueError(f"sample_rows: expected [rows, vocab], got {tuple(logits.shape)}")
+    lg = logits if logits.stride(1) == 1 else logits.contiguous()
+    rows, vocab = lg.shape
+    u = uniforms.to(torch.float32).contiguous()
+    if u.numel() != rows:
+        raise ValueError("sample_rows: one uniform per row")
+    ids = torch.empty(rows, dtype=torch.long, device=logits.device)
+    status = torch.zeros(1, dtype=torch.int32, device=logits.device)
+    stride = lg.stride(0) if rows > 1 else vocab
+    rc = _native.lib().pkv_sample_rows(ids.data_ptr(), lg.data_ptr(), rows, vocab, stride,
+                                       float(temperature), int(top_k), float(top_p),
+                                       u.data_ptr(), _native.dtype_code(lg.dtype),
+                                       status.data_ptr(), _native.stream_ptr(logits.device))
+    _native.check(rc, "sample_rows")
+    return ids, status
+
+
 class FusedRows:
     """Row-concatenated weights (and biases) of several nn.Linear modules
     sharing an input, so one GEMM computes all of their outputs. The

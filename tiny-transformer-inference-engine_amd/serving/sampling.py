@@ -45,7 +45,17 @@ def apply_top_p(logits, top_p):
     return torch.full_like(logits, float("-inf")).scatter(-1, order, sorted_logits)
 
 
+# top_k range of the fused sampling kernel (pkv_sample_rows)
+KERNEL_MAX_TOP_K = 64
+
+
 def sample(logits, temperature=1.0, top_k=0, top_p=1.0):
+    """On a ROCm device with 1 <= top_k <= 64: one HIP kernel per step
+    (fused_ops.sample_rows) draws every row by inverse CDF at a uniform from
+    torch's generator; its status word is read once (the reference's own
+    finiteness checks synchronise too) to raise the reference's errors, and
+    a row the kernel declines (massive ties at the threshold) sends the
+    call to the framework path below."""
     if logits.ndim != 2 or logits.shape[-1] == 0:
         raise ValueError("logits must have shape [batch, vocab] with non-empty vocab")
     if not math.isfinite(temperature) or temperature <= 0:
@@ -54,6 +64,17 @@ def sample(logits, temperature=1.0, top_k=0, top_p=1.0):
         raise ValueError("top_k must be >= 0")
     if not 0 < top_p <= 1:
         raise ValueError("top_p must be in (0, 1]")
+    if (logits.is_cuda and 1 <= top_k <= KERNEL_MAX_TOP_K
+            and logits.dtype in (torch.float32, torch.bfloat16, torch.float16)):
+        u = torch.rand(logits.shape[0], device=logits.device, dtype=torch.float32)
+        ids, status = fused_ops.sample_rows(logits, temperature, top_k, top_p, u)
+        flags = int(status.item())
+        if flags & fused_ops._native.PKV_STATUS_NONFINITE:
+            raise ValueError("logits contain NaN or infinity")
+        if flags & fused_ops._native.PKV_STATUS_BAD_DISTRIBUTION:
+            raise ValueError("sampling produced an invalid probability distribution")
+        if not flags & fused_ops._native.PKV_STATUS_SAMPLE_OVERFLOW:
+            return ids[:, None]
     logits = logits.float()
     if not torch.isfinite(logits).all():
         raise ValueError("logits contain NaN or infinity")
