@@ -10,6 +10,8 @@
 // unaligned, then vectors, then a scalar tail), keeping per thread the best
 // (value, index); the candidates are combined across the wavefront by lane
 // swaps and across wavefronts through LDS with the same ordering rule.
+#include <type_traits>
+
 #include "pkv_internal.h"
 
 namespace pkv {
@@ -183,24 +185,32 @@ __global__ __launch_bounds__(kSmpThreads) void sample_rows_kernel(
     s_pick = 0x7fffffff;
   }
   // 1. thread maxima and finiteness
-  // (kSmpUnroll loads of a thread in flight together: indices past the row
-  // are clamped onto its last element and their values dropped)
+  // (kSmpUnroll loads of a thread in flight together, indices past the row
+  // clamped onto its last element; the arithmetic is branch-free so the
+  // compiler can interleave the elements' division chains; temperature 1
+  // divides exactly by skipping the division)
   float mx = -INFINITY;
   int flags = 0;
-  for (int j0 = tid; j0 < vocab; j0 += kSmpUnroll * kSmpThreads) {
-    float xv[kSmpUnroll];
+  auto pass1 = [&](auto unit) {
+    for (int j0 = tid; j0 < vocab; j0 += kSmpUnroll * kSmpThreads) {
+      float xv[kSmpUnroll];
 #pragma unroll
-    for (int q = 0; q < kSmpUnroll; ++q) xv[q] = (float)row[min(j0 + q * kSmpThreads, vocab - 1)];
+      for (int q = 0; q < kSmpUnroll; ++q) xv[q] = (float)row[min(j0 + q * kSmpThreads, vocab - 1)];
 #pragma unroll
-    for (int q = 0; q < kSmpUnroll; ++q) {
-      if (j0 + q * kSmpThreads < vocab) {
-        const float y = xv[q] / temperature;
-        if (!isfinite(xv[q])) flags |= PKV_STATUS_NONFINITE;
-        else if (!isfinite(y)) flags |= PKV_STATUS_BAD_DISTRIBUTION;
-        mx = fmaxf(mx, y);
+      for (int q = 0; q < kSmpUnroll; ++q) {
+        const bool in = j0 + q * kSmpThreads < vocab;
+        const float y = decltype(unit)::value ? xv[q] : xv[q] / temperature;
+        flags |= (in && !isfinite(xv[q])) ? PKV_STATUS_NONFINITE : 0;
+        flags |= (in && isfinite(xv[q]) && !isfinite(y)) ? PKV_STATUS_BAD_DISTRIBUTION : 0;
+        mx = in ? fmaxf(mx, y) : mx;
       }
     }
-  }
+  };
+  const bool unit_temp = temperature == 1.f;
+  if (unit_temp)
+    pass1(std::integral_constant<bool, true>{});
+  else
+    pass1(std::integral_constant<bool, false>{});
   key[tid] = mx;
   idx[tid] = tid;
   __syncthreads();
@@ -218,23 +228,36 @@ __global__ __launch_bounds__(kSmpThreads) void sample_rows_kernel(
     return;
   }
   // 3. candidates >= t0, sorted
-  for (int j0 = tid; j0 < vocab; j0 += kSmpUnroll * kSmpThreads) {
-    float xv[kSmpUnroll];
+  auto pass2 = [&](auto unit) {
+    for (int j0 = tid; j0 < vocab; j0 += kSmpUnroll * kSmpThreads) {
+      float yv[kSmpUnroll];
 #pragma unroll
-    for (int q = 0; q < kSmpUnroll; ++q) xv[q] = (float)row[min(j0 + q * kSmpThreads, vocab - 1)];
+      for (int q = 0; q < kSmpUnroll; ++q) yv[q] = (float)row[min(j0 + q * kSmpThreads, vocab - 1)];
 #pragma unroll
-    for (int q = 0; q < kSmpUnroll; ++q) {
-      const int j = j0 + q * kSmpThreads;
-      const float y = xv[q] / temperature;
-      if (j < vocab && y >= t0) {
+      for (int q = 0; q < kSmpUnroll; ++q)
+        if (!decltype(unit)::value) yv[q] = yv[q] / temperature;
+      unsigned hit = 0;
+#pragma unroll
+      for (int q = 0; q < kSmpUnroll; ++q)
+        hit |= (j0 + q * kSmpThreads < vocab && yv[q] >= t0) ? 1u << q : 0u;
+      while (hit) {  // rare: the few values >= t0
+        const int q = __builtin_ctz(hit);
+        hit &= hit - 1;
+        float y = yv[0];
+#pragma unroll
+        for (int r = 1; r < kSmpUnroll; ++r) y = r == q ? yv[r] : y;
         const int at = atomicAdd(&s_cnt, 1);
         if (at < kSmpCand) {
           key[at] = y;
-          idx[at] = j;
+          idx[at] = j0 + q * kSmpThreads;
         }
       }
     }
-  }
+  };
+  if (unit_temp)
+    pass2(std::integral_constant<bool, true>{});
+  else
+    pass2(std::integral_constant<bool, false>{});
   __syncthreads();
   const int nc = s_cnt;
   if (nc > kSmpCand) {
@@ -310,19 +333,21 @@ __global__ __launch_bounds__(kSmpThreads) void sample_rows_kernel(
   }
   const float target = uniforms[blockIdx.x] * smp_wave_sum(tot_l);
   // inverse CDF in vocabulary order: token i's cumulative start is the sum
-  // of the kept probabilities of smaller indices
-  int pick = 0x7fffffff, last = -1;
+  // of the kept probabilities of smaller indices. The probabilities replace
+  // the values in LDS (this wavefront's LDS accesses complete in order), and
+  // the kept tokens are spread over the lanes.
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int i = i0 + e;
-    if (i < nk) {
-      const int my = idx[i];
-      float c = 0.f;
-      for (int j = 0; j < nk; ++j)
-        if (idx[j] < my) c += expf(key[j] - m) / zk;
-      if (c + pv[e] > target) pick = min(pick, my);
-      last = max(last, my);
-    }
+  for (int e = 0; e < PER; ++e)
+    if (i0 + e < nk) key[i0 + e] = pv[e];
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  int pick = 0x7fffffff, last = -1;
+  for (int i = lane; i < nk; i += 64) {
+    const int my = idx[i];
+    float c = 0.f;
+    for (int j = 0; j < nk; ++j) c += idx[j] < my ? key[j] : 0.f;
+    if (c + key[i] > target) pick = min(pick, my);
+    last = max(last, my);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
