@@ -331,6 +331,18 @@ def run_profile(args, torch):
         args.warmup = 1
         run_model(args, torch)
         return
+    if args.profile == "sampling":
+        # the scheduler's sampling step at config 4's batch: 128 rows of a
+        # 50257-entry bf16 vocabulary, top_k 32, top_p 0.9, temperature 1
+        from serving import fused_ops
+        g = torch.Generator(device=dev).manual_seed(0)
+        logits = torch.randn(128, 50257, generator=g, device=dev).bfloat16()
+        u = torch.rand(128, generator=g, device=dev)
+        for _ in range(args.profile_iters):
+            fused_ops.sample_rows(logits, 1.0, 32, 0.9, u)
+        torch.cuda.synchronize()
+        log(f"profile sampling: {args.profile_iters} launches")
+        return
     if args.profile == "cfg5mixed":
         p = workloads.cfg5_mixed_problem(dev, chunk=128, seed=0, bs=16)
         out = torch.empty_like(p.q)
@@ -386,7 +398,7 @@ def main():
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
-    ap.add_argument("--profile", choices=["cfg4", "cfg5", "cfg5mixed", "model"], default=None,
+    ap.add_argument("--profile", choices=["cfg4", "cfg5", "cfg5mixed", "model", "sampling"], default=None,
                     help="run only the decode-attention launches of this workload "
                          "(a rocprofv3 target); no JSON line")
     ap.add_argument("--profile-iters", type=int, default=20)
