@@ -221,3 +221,46 @@ def test_persistent_random_length_mixes(seed):
         torch.cuda.synchronize()
         check(out, lse, eo, el, f"mix seed {seed} rep {rep} part_tokens {pt}")
         assert int(_counters().abs().sum()) == 0, "arrival counters not reset"
+
+
+@pytest.mark.parametrize("pt", [STATIC, 512])
+def test_in_kernel_merges_replayed_from_a_hip_graph(pt):
+    """The decode launch with its in-kernel merges (arrival counters in the
+    workspace, reset by the last contributor) captured in a HIP graph and
+    replayed with eager work and host synchronisations in between: every
+    replay equals the eager result bit for bit, and the counters are zero
+    after each."""
+    g, d = 32, 128
+    rng = np.random.default_rng(31)
+    lens = np.minimum(rng.lognormal(np.log(900), 1.0, size=64).astype(int) + 1, 6000)
+    p = workloads.decode_problem(lens, g, 1, d, 16, 16384, torch.bfloat16, DEV, seed=31)
+    out = torch.empty_like(p.q)
+    lse = torch.empty(len(lens), g, device=DEV)
+    mk = int(max(lens))
+
+    def call():
+        paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, out=out,
+                         lse=lse, max_kv_len=mk, part_tokens=pt)
+
+    call()
+    torch.cuda.synchronize()
+    eo, el = out.clone(), lse.clone()
+    check(eo, el, *oracle(p), "eager")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        call()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    torch.cuda.synchronize()
+    for k in range(4):
+        out.fill_(7.0)
+        lse.fill_(7.0)
+        _ = torch.randn(1024, 1024, device=DEV).sum()  # unrelated eager work
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eo) and torch.equal(lse, el), f"replay {k} differs"
+        assert int(_counters().abs().sum()) == 0, f"replay {k}: counters not reset"
