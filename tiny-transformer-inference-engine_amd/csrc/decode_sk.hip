@@ -10,14 +10,17 @@
 // distribution (one that covers many short sequences streams fewer chunks):
 //   - a sequence that lies entirely inside one share is finished in place
 //     (its wavefronts' states are merged through LDS and written out);
-//   - a sequence cut by share boundaries gets one partial (m, l, O) per
+//   - a sequence cut by share boundaries gets one partial (m, l, O/l) per
 //     workgroup that touches it (its first or last segment there, so at most
-//     two per workgroup), written with plain stores; the workgroup holding
-//     its first chunk also records which workgroups contributed.
-// sk_merge_kernel, launched right after on the same stream (the kernel
-// boundary makes the partials visible), combines the partials of every cut
-// sequence in parallel over (sequence, output slice). Nothing waits on
-// another workgroup, so the scheme cannot deadlock whatever the residency.
+//     two per workgroup), written through to memory; each contributor then
+//     counts itself in on the sequence's arrival counter, and the one that
+//     completes the count merges every partial (in contributor order) and
+//     writes the row. Nothing waits on another workgroup, so the scheme
+//     cannot deadlock whatever the residency.
+// (With kInKernelMerge = false the partials are written with plain stores,
+// the workgroup holding a cut sequence's first chunk records its
+// contributors, and sk_merge_kernel, launched right after on the same
+// stream, combines them; kept for comparison.)
 // The per-chunk pipeline is mfma_decode_common.h. Semantics are those of
 // pagedattn.forward (kernels/pagedattn/pagedattn.cu:142-447) for q_len = 1.
 #include "mfma_decode_common.h"
