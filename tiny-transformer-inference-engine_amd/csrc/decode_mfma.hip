@@ -11,7 +11,10 @@
 // ...) through the pipeline of mfma_decode_common.h, so no workgroup barrier
 // sits in the main loop. At the end the 4 wavefronts merge their
 // (max, sum, O) through LDS and the workgroup writes the final row (one
-// partition) or a split-K partial that merge_kernel (attention.hip) combines.
+// partition) or a split-K partial. With arrival counters (AttnArgs::merge_ctr)
+// the partition that completes a sequence's count merges its partials in
+// the same launch; without them (prefill tiles, very large batches)
+// merge_kernel (attention.hip) combines them in a second launch.
 // The grid is sequence-fastest: workgroups are dispatched round-robin over
 // the XCDs, so consecutive workgroups of different sequences spread the
 // partitions of short and long sequences over all of them.
