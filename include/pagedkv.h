@@ -104,6 +104,12 @@ extern "C" {
 #define PKV_STATUS_BAD_DISTRIBUTION 64 /* sampling: logit / temperature overflowed */
 #define PKV_STATUS_SAMPLE_OVERFLOW 128 /* sampling: too many ties at the top-k
                                           threshold for the kernel (id -1)    */
+#define PKV_STATUS_DIRTY_WORKSPACE 256 /* attention: an arrival counter of the
+                                          workspace was not zero when the call
+                                          started (workspace not zero-filled, or
+                                          shared by overlapping calls); rows of
+                                          sequences split across workgroups may
+                                          be missing or wrong                 */
 
 /* Library version (PKV_VERSION). */
 int pkv_version(void);

@@ -96,3 +96,51 @@ def test_graph_rejects_prefill_batch():
     meta = pack_batch_meta([[1, 2]], [0, 3], [0, 1, 2], 3, torch.device(DEV), 16)
     with pytest.raises(ValueError):
         DecodeStepGraph(model, pool, meta, torch.zeros(3, dtype=torch.long, device=DEV))
+
+
+def test_graph_keeps_its_workspace_when_eager_calls_grow_theirs():
+    """Capture, then an unrelated eager attention call that needs a larger
+    process-wide workspace (so the caching allocator frees the old one),
+    then allocations that may reuse the freed memory (filled with non-zero
+    words, which would look like dirty arrival counters): every replay must
+    still equal the eager step bit for bit."""
+    from serving.fake_paged_attn import paged_mqa_decode
+    dtype = torch.bfloat16
+    cfg = ModelConfig(vocab_size=4096, d_model=1024, num_layers=2, num_heads=16,
+                      num_kv_heads=1, max_seq_len=4096)
+    n_seq, steps = 32, 4
+    print(f"[graph step] workspace growth after capture, n_seq={n_seq}", flush=True)
+    torch.manual_seed(0)
+    model = PagedTransformer(cfg).to(DEV, dtype).eval()
+    lens = workloads.lengths_uniform(n_seq, 256, 2048, seed=4)
+    pool_a, meta_a, ids_a = make_batch(cfg, dtype, n_seq, lens, 16, 4096, steps, seed=6)
+    pool_b, meta_b, ids_b = clone_batch(pool_a, meta_a, ids_a)
+    graph = DecodeStepGraph(model, pool_b, meta_b, ids_b, warmup=1)
+    with torch.no_grad():
+        logits = model.forward_step(ids_a, pool_a, meta_a)
+    ids_a = logits.argmax(-1)
+    for t in (meta_a.positions, meta_a.start_pos, meta_a.seq_lens):
+        t.add_(1)
+    # grow the process-wide workspace (persistent-kernel problem, ~9 MB of
+    # scratch), release the old buffer, and reuse freed memory
+    prob = workloads.cfg5_problem(torch.device(DEV), seed=1, bs=16)
+    paged_mqa_decode(prob.q, prob.k_pool, prob.v_pool, prob.block_tables, prob.seq_lens,
+                     max_kv_len=int(prob.lens.max()))
+    torch.cuda.synchronize()
+    del prob
+    torch.cuda.empty_cache()
+    junk = [torch.full((1 << 18,), 7, dtype=torch.int32, device=DEV) for _ in range(64)]
+    torch.cuda.synchronize()
+    for k in range(steps):
+        toks = graph.replay()
+        torch.cuda.synchronize()
+        with torch.no_grad():
+            ref = model.forward_step(ids_a, pool_a, meta_a)
+        ids_a = ref.argmax(-1)
+        for t in (meta_a.positions, meta_a.start_pos, meta_a.seq_lens):
+            t.add_(1)
+        torch.cuda.synchronize()
+        assert torch.equal(toks, ids_a), f"replay {k}: tokens differ"
+        assert torch.equal(graph.logits, ref), f"replay {k}: logits differ"
+    assert torch.equal(pool_b.kv, pool_a.kv), "pools differ after the replays"
+    del junk

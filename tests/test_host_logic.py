@@ -60,6 +60,23 @@ def test_failed_free_changes_nothing():
     assert a.num_free == before
 
 
+def test_failed_free_rolls_back_and_names_first_bad_id():
+    # the first bad id in list order decides the message (the reference
+    # validates in list order); the ids before it stay in use
+    a = BlockAllocator(8)
+    b1, b2, b3 = a.allocate_n(3)
+    with pytest.raises(ValueError, match=f"double free of block {b2}"):
+        a.free([b1, b2, b3, b2])
+    with pytest.raises(ValueError, match="invalid block id 9"):
+        a.free([b3, 9, b1])
+    assert a.num_free == 4
+    # nothing was released: the next allocation is a fresh id, and every
+    # original id can still be freed exactly once
+    assert a.allocate() == 4
+    a.free([b3, b1, b2])
+    assert [a.allocate() for _ in range(3)] == [b2, b1, b3]
+
+
 def test_allocation_order_is_ascending_then_lifo(kats):
     c = kats["allocator_order"]
     a = BlockAllocator(c["num_blocks"])
@@ -128,6 +145,10 @@ def test_pool_slot_mapping_asserts():
         pool.make_slot_mapping(10, 7, [3])
     with pytest.raises(AssertionError, match="block 0"):
         pool.make_slot_mapping(0, 20, [4, 0])
+    # a block id past the pool: the reference's index_put would raise at
+    # write time; here the mapping refuses it (the device write would skip it)
+    with pytest.raises(IndexError, match="out of range"):
+        pool.make_slot_mapping(0, 20, [4, 16])
 
 
 def test_pool_write_checks_then_refuses_cpu():

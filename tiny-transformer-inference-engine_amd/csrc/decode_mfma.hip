@@ -236,6 +236,10 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     const int old = fetch_add_agent(ctr, 1);
     s_last = old == g.nparts - 1;
     if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // a counter that started at c != 0 shows a value outside [0, nparts) to
+    // at least one partition (the largest it sees is c + nparts - 1, the
+    // smallest c): never silent
+    if ((old < 0 || old >= g.nparts) && a.status) atomicOr(a.status, PKV_STATUS_DIRTY_WORKSPACE);
   }
   __syncthreads();
   if (!s_last) return;

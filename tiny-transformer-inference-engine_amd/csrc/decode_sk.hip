@@ -472,6 +472,10 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
           const int old = fetch_add_agent(ctr, 1);
           s_last = old == w_last - w_first;
           if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          // a dirty counter (start value c != 0) shows a value outside
+          // [0, contributors) to at least one contributor
+          if ((old < 0 || old > w_last - w_first) && a.status)
+            atomicOr(a.status, PKV_STATUS_DIRTY_WORKSPACE);
         }
         __syncthreads();
         if (s_last)

@@ -6,6 +6,7 @@ missing or when a tensor is not on a ROCm device. There is no CPU fallback.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -30,6 +31,7 @@ PKV_STATUS_BAD_POS = 16
 PKV_STATUS_NONFINITE = 32
 PKV_STATUS_BAD_DISTRIBUTION = 64
 PKV_STATUS_SAMPLE_OVERFLOW = 128
+PKV_STATUS_DIRTY_WORKSPACE = 256
 # part_tokens values selecting a persistent decode kernel: the one the
 # library prefers, the one with static equal shares, or the dynamically
 # scheduled one (largest-first work items drawn from a counter; up to 1024
@@ -190,3 +192,28 @@ class Workspace:
 
 
 WORKSPACE = Workspace()
+
+_scopes = threading.local()
+
+
+def current_workspace() -> Workspace:
+    """The Workspace the attention wrappers use on this thread: the innermost
+    workspace_scope, else the process-wide WORKSPACE."""
+    stack = getattr(_scopes, "stack", None)
+    return stack[-1] if stack else WORKSPACE
+
+
+@contextlib.contextmanager
+def workspace_scope(ws: Workspace):
+    """Route the attention wrappers' scratch to `ws` inside the block. A HIP
+    graph captures the raw address of the buffer it is given, so a captured
+    step needs a workspace no later eager call can grow (and thereby free);
+    serving.graph_step holds one per graph for the graph's lifetime."""
+    stack = getattr(_scopes, "stack", None)
+    if stack is None:
+        stack = _scopes.stack = []
+    stack.append(ws)
+    try:
+        yield ws
+    finally:
+        stack.pop()

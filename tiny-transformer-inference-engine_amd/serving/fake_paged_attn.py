@@ -61,7 +61,7 @@ def _launch(q, k_pool, v_pool, block_tables, seq_lens, queryloc, n_seq,
     L = _native.lib()
     ws_bytes = L.pkv_attention_workspace_bytes(
         n_seq, max_q_len, hq, hkv, d, max_blk, bs, max_kv_len, part_tokens, code)
-    ws = _native.WORKSPACE.get(q.device, ws_bytes)
+    ws = _native.current_workspace().get(q.device, ws_bytes)
     rc = L.pkv_paged_attention(
         out.data_ptr(), _native.ptr(lse), q.data_ptr(), k_pool.data_ptr(),
         v_pool.data_ptr(), nb, bs, block_tables.data_ptr() if max_blk else None,
@@ -238,7 +238,7 @@ def paged_attention_append_meta(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
     ws_bytes = L.pkv_attention_workspace_bytes(
         meta.num_seqs, meta.max_q_len, hq, pool.num_kv_heads, d, max_blk, pool.block_size,
         meta.max_kv_len, 0, code)
-    ws = _native.WORKSPACE.get(q.device, ws_bytes)
+    ws = _native.current_workspace().get(q.device, ws_bytes)
     status = pool._status()
     rc = L.pkv_paged_attention_append(
         out.data_ptr(), _native.ptr(lse), q.data_ptr(), kp.data_ptr(), vp.data_ptr(),

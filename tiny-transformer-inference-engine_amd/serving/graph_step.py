@@ -16,12 +16,18 @@ tensor in place (same shape) before the replay. The attention plan (split-K
 partition count) is fixed at capture for meta.max_kv_len; the kernels stay
 exact for longer contexts (a longer partition per workgroup), so capture
 with the bound the batch will reach.
+
+The graph owns its scratch: the split-K partials and arrival counters of
+the attention live in a workspace created for this graph, sized by the eager
+warm-up steps and kept for the graph's lifetime. Eager attention calls made
+between replays use the process-wide workspace, so when they grow (and free)
+it, the buffer the graph captured is unaffected.
 """
 from __future__ import annotations
 
 import torch
 
-from . import fused_ops
+from . import _native, fused_ops
 
 
 class DecodeStepGraph:
@@ -44,18 +50,20 @@ class DecodeStepGraph:
         self.model, self.pool, self.meta = model, pool, meta
         self.ids = ids.clone()
         self.logits = None
-        # eager steps on a side stream before capture (library handles,
-        # workspace and caching-allocator pools are created here)
+        self.workspace = _native.Workspace()
+        # eager steps on a side stream before capture (library handles, this
+        # graph's workspace and caching-allocator pools are created here)
         side = torch.cuda.Stream(device=ids.device)
         side.wait_stream(torch.cuda.current_stream(ids.device))
-        with torch.cuda.stream(side), torch.no_grad():
-            for _ in range(max(warmup, 1)):
-                self._step()
-        torch.cuda.current_stream(ids.device).wait_stream(side)
-        torch.cuda.synchronize(ids.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph), torch.no_grad():
-            self.logits = self._step()
+        with _native.workspace_scope(self.workspace):
+            with torch.cuda.stream(side), torch.no_grad():
+                for _ in range(max(warmup, 1)):
+                    self._step()
+            torch.cuda.current_stream(ids.device).wait_stream(side)
+            torch.cuda.synchronize(ids.device)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph), torch.no_grad():
+                self.logits = self._step()
 
     def _step(self):
         logits = self.model.forward_step(self.ids, self.pool, self.meta)

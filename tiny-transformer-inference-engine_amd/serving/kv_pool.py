@@ -87,6 +87,13 @@ class KVPool:
         slot = bt[p // self.block_size] * self.block_size + p % self.block_size
         assert np.all(slot >= self.block_size), \
             f"slot mapping touches block 0, which is reserved: {slot[slot < self.block_size]}"
+        # the reference's index_put in write() raises on a slot past the
+        # pool; write() here skips such a slot on the device (and raises only
+        # under debug, after a synchronisation), so catch it on the host
+        # where the mapping is built
+        if slot.size and int(slot.max()) >= self.num_slots:
+            raise IndexError(
+                f"slot {int(slot.max())} out of range for a pool of {self.num_slots} slots")
         return torch.from_numpy(slot).to(self.device)
 
     # ------------------------------------------------------------------

@@ -3,8 +3,9 @@ from __future__ import annotations
 
 
 class Sequence:
-    """One request's state: its tokens and the physical blocks it owns
-    (reference: serving/sequence.py:1-34)."""
+    """A request being served: the token ids seen so far (prompt, then
+    generated) and the block table that maps its token positions to
+    physical KV blocks (reference: serving/sequence.py:1-34)."""
 
     def __init__(self, seq_id: int, prompt_token_ids: list[int], block_size: int):
         self.seq_id = seq_id
