@@ -76,16 +76,12 @@ extern "C" {
 #define PKV_DTYPE_F16 1
 #define PKV_DTYPE_BF16 2
 
-/* part_tokens values of pkv_paged_attention selecting a persistent decode
+/* part_tokens values of pkv_paged_attention selecting the persistent decode
    kernel where it applies (bf16/f16, one query per sequence, 16 or 32
-   query heads per kv head, d = 64 or 128): PKV_PART_PERSISTENT the one the
-   library prefers (currently the static one), PKV_PART_STATIC the one with
-   static equal shares, PKV_PART_DYNAMIC the dynamically scheduled one (up
-   to 1024 sequence x kv head pairs, block_size >= 16; else the static
-   one). */
+   query heads per kv head, d = 64 or 128): PKV_PART_PERSISTENT, and
+   PKV_PART_STATIC, its name for its static equal shares (the same kernel). */
 #define PKV_PART_PERSISTENT (-1)
 #define PKV_PART_STATIC (-2)
-#define PKV_PART_DYNAMIC (-3)
 
 #define PKV_OK 0
 #define PKV_ERR_INVALID (-1)     /* bad argument (shape, null pointer, ...) */
@@ -192,10 +188,8 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
  * capacity) must bound every kv_len; `part_tokens` is the split-K
  * partition length (0: automatic, the persistent kernel for context bounds
  * of 4096 tokens and more where it applies, else fixed partitions;
- * PKV_PART_STATIC: persistent workgroups each taking an equal share of all
- * context chunks; PKV_PART_DYNAMIC: one persistent workgroup per CU drawing
- * work items (whole sequences, pieces of long ones) largest first;
- * PKV_PART_PERSISTENT: the persistent kernel the library prefers).
+ * PKV_PART_PERSISTENT or PKV_PART_STATIC: persistent workgroups each taking
+ * an equal share of all context chunks; other negative values are invalid).
  * Workspace: pkv_attention_workspace_bytes().
  */
 int pkv_paged_attention(void* out, float* lse, const void* q,

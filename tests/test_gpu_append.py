@@ -27,9 +27,13 @@ def bits(t):
 
 
 def shuffled_allocator(num_blocks, seed):
+    """An allocator that hands its blocks out in a random order: every block
+    is taken once and returned in a shuffled order (freed blocks come back
+    most recently freed first), through the public interface only."""
     a = BlockAllocator(num_blocks)
     rng = np.random.default_rng(seed)
-    rng.shuffle(a._free)
+    ids = a.allocate_n(a.num_free)
+    a.free([int(x) for x in rng.permutation(ids)])
     return a
 
 

@@ -1,7 +1,7 @@
-"""The MFMA decode kernels (the split-K partition form, the default; the
-static-share persistent form, part_tokens = PART_STATIC; the dynamically
-scheduled persistent form, PART_DYNAMIC; PART_PERSISTENT, the one the
-library prefers) against the fp64 oracle, on the shapes that stress their
+"""The MFMA decode kernels (the split-K partition form, part_tokens > 0 or
+automatic below long context bounds; the persistent form with equal shares
+of all context chunks, part_tokens = PART_PERSISTENT or PART_STATIC)
+against the fp64 oracle, on the shapes that stress their
 work decomposition:
 
   - one very long sequence, cut by every workgroup share (all partials,
@@ -24,7 +24,7 @@ from serving.fake_paged_attn import paged_attn_fwd, paged_mqa_decode
 pytestmark = pytest.mark.gpu
 SK = _native.PART_PERSISTENT
 STATIC = _native.PART_STATIC
-DYN = _native.PART_DYNAMIC
+PART = 512  # the split-K partition kernel, 512-token partitions
 DEV = "cuda"
 SHAPES = [(16, 64), (32, 128), (16, 128), (32, 64)]  # (heads per kv head, D)
 
@@ -53,7 +53,7 @@ def check(out, lse, eo, el, what):
 
 
 @pytest.mark.parametrize("g,d", SHAPES)
-@pytest.mark.parametrize("part_tokens", [SK, STATIC, DYN, 0, 512])
+@pytest.mark.parametrize("part_tokens", [SK, STATIC, 0, 512])
 def test_single_long_sequence(g, d, part_tokens):
     print(f"[decode long] g={g} d={d} part={part_tokens}", flush=True)
     p = workloads.decode_problem([30000], g, 1, d, 16, 2048, torch.bfloat16, DEV, seed=11)
@@ -77,7 +77,7 @@ def test_many_short_and_empty_sequences_repeated(g, d):
     seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
     eo, el = oracle(p, seq_lens)
     for rep in range(4):
-        pt = DYN if rep % 2 == 0 else STATIC
+        pt = PART if rep % 2 == 0 else STATIC
         lse = torch.empty(len(lens), g, device=DEV)
         out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
                                part_tokens=pt)
@@ -101,7 +101,7 @@ def test_gqa_two_kv_heads_and_missing_queries(dtype):
     eo, el = ref.paged_attention(np64(q), np64(p.k_pool), np64(p.v_pool),
                                  p.block_tables.cpu().numpy(), p.seq_lens.cpu().numpy(),
                                  qsl.cpu().numpy())
-    for pt in (0, SK, STATIC, DYN):
+    for pt in (0, SK, STATIC, PART):
         O = torch.empty_like(q)
         L = torch.empty(T, g * hkv, device=DEV)
         paged_mqa_decode(q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, out=O, lse=L,
@@ -113,8 +113,6 @@ def test_gqa_two_kv_heads_and_missing_queries(dtype):
 def test_cfg4_and_cfg5_kernels_agree():
     for name, p in [("cfg4", workloads.cfg4_problem(DEV)), ("cfg5", workloads.cfg5_problem(DEV))]:
         mk = int(p.lens.max())
-        c = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
-                             part_tokens=DYN)
         a = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
                              part_tokens=SK)
         b = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, max_kv_len=mk,
@@ -122,11 +120,9 @@ def test_cfg4_and_cfg5_kernels_agree():
         torch.cuda.synchronize()
         diff = (a.float() - b.float()).abs().max().item()
         assert diff <= 2e-2, f"{name}: persistent vs partition kernel differ by {diff}"
-        diff = (c.float() - b.float()).abs().max().item()
-        assert diff <= 2e-2, f"{name}: dynamic persistent vs partition kernel differ by {diff}"
     
 
-@pytest.mark.parametrize("pt", [SK, STATIC, DYN])
+@pytest.mark.parametrize("pt", [SK, STATIC, PART])
 def test_records_of_previous_call_do_not_leak(pt):
     """A call where every sequence is split across workgroups, then a call on
     the same workspace where some of those sequences have no query: rows are
@@ -156,16 +152,15 @@ def test_records_of_previous_call_do_not_leak(pt):
 
 
 def _counters():
-    """The persistent kernels' counters in the library workspace on this
-    device: the dynamic kernel's draw and arrival counters (first 8 KiB) and
-    the static kernel's per-sequence arrival counters (the last int of each
-    16-byte record after them)."""
+    """The decode kernels' arrival counters in the library workspace on this
+    device: the partition kernel's (first 8 KiB) and the persistent kernel's
+    per-sequence ones (the last int of each 16-byte record after them)."""
     buf = _native.WORKSPACE._bufs[torch.cuda.current_device()]
     recs = buf[8 * 1024: 256 * 1024].view(torch.int32).view(-1, 4)
     return torch.cat([buf[: 8 * 1024].view(torch.int32), recs[:, 3]])
 
 
-@pytest.mark.parametrize("pt", [STATIC, DYN])
+@pytest.mark.parametrize("pt", [STATIC, PART])
 def test_cut_sequences_alternating_inputs_and_counters_reset(pt):
     """Pieces of long sequences are merged inside the kernel by the last
     workgroup to arrive, from partials other workgroups (on other XCDs)
@@ -214,7 +209,7 @@ def test_persistent_random_length_mixes(seed):
     seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
     eo, el = oracle(p, seq_lens)
     for rep in range(4):
-        pt = DYN if rep % 2 == 0 else STATIC
+        pt = PART if rep % 2 == 0 else STATIC
         lse = torch.empty(n, g, device=DEV)
         out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
                                part_tokens=pt)

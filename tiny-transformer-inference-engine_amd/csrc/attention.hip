@@ -338,18 +338,8 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   // leave the long sequences' workgroups running alone) take the persistent
   // kernel, which gives every workgroup the same share of the actual work
   const bool persistent = part_tokens == PKV_PART_PERSISTENT ||
-                          part_tokens == PKV_PART_STATIC || part_tokens == PKV_PART_DYNAMIC ||
+                          part_tokens == PKV_PART_STATIC ||
                           (part_tokens == 0 && kv_bound >= kSkAutoKv);
-  if (mfma && part_tokens == PKV_PART_DYNAMIC && virt <= kDynMaxSeq && block_size >= 16) {
-    // dynamic persistent kernel: piece partials in item-index slots
-    p.kind = 4;
-    p.rows = group;
-    p.tiles_max = 1;
-    p.part_tokens = 0;
-    p.parts_max = 1;
-    p.ws_bytes = dyn_workspace_bytes(group, d);
-    return p;
-  }
   if (mfma && persistent && sk_fits(virt, max_blk)) {
     // persistent kernel: partials of at most two segments per workgroup
     p.kind = 2;
@@ -455,18 +445,10 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
     k.n_wg = 2 * device_cu_count() < kSkMaxWg ? 2 * device_cu_count() : kSkMaxWg;
     k.seg_cost = kSkSegCost;
     char* ws = reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes;
-    k.recs = reinterpret_cast<int4*>(ws + kWsDynCtrBytes);
+    k.recs = reinterpret_cast<int4*>(ws + kWsCtrBytes);
     k.part_o = reinterpret_cast<_Float16*>(a.ws_o);
     k.part_ml = reinterpret_cast<float*>(k.part_o + (size_t)kSkMaxWg * 2 * a.group * a.d);
     return launch_decode_sk(a, k, dtype, stream);
-  }
-  if (p.kind == 4) {
-    DynArgs k{};
-    k.piece = kDynPiece;
-    k.ctr = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes);
-    k.part_o = reinterpret_cast<_Float16*>(a.ws_o);
-    k.part_ml = reinterpret_cast<float*>(k.part_o + (size_t)kDynItemCap * a.group * a.d);
-    return launch_decode_dyn(a, k, dtype, stream);
   }
   if (p.kind == 1) {
     if (dtype == PKV_DTYPE_BF16) return launch_mfma<bf16>(a, p, dtype, stream);

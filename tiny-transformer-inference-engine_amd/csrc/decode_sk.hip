@@ -17,10 +17,6 @@
 //     completes the count merges every partial (in contributor order) and
 //     writes the row. Nothing waits on another workgroup, so the scheme
 //     cannot deadlock whatever the residency.
-// (With kInKernelMerge = false the partials are written with plain stores,
-// the workgroup holding a cut sequence's first chunk records its
-// contributors, and sk_merge_kernel, launched right after on the same
-// stream, combines them; kept for comparison.)
 // The per-chunk pipeline is mfma_decode_common.h. Semantics are those of
 // pagedattn.forward (kernels/pagedattn/pagedattn.cu:142-447) for q_len = 1.
 #include "mfma_decode_common.h"
@@ -126,11 +122,6 @@ __device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
   return __builtin_amdgcn_readfirstlane(total);
 }
 
-// Cut sequences are merged inside the launch by the workgroup that stores
-// the last of their partials (true), or by sk_merge_kernel launched after it
-// (false).
-constexpr bool kInKernelMerge = true;
-
 __device__ __forceinline__ uint64_t ld_agent64(const void* p) {
   return __hip_atomic_load(static_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -148,8 +139,7 @@ __device__ __forceinline__ int64_t cut_slot(int ww, int w_first, int r_slot) {
 // the result does not depend on which contributor merges): thread tid owns
 // head tid / TPH and the float4 columns cq + TPH q, the (max, sum) pair of
 // its head is read once per contributor, and every load of a batch of kMB
-// contributors is issued before any is consumed. The arithmetic is
-// sk_merge_kernel's. Loads are device-coherent (they bypass this XCD's L2:
+// contributors is issued before any is consumed. Loads are device-coherent (they bypass this XCD's L2:
 // the partials were written through from other XCDs during this launch).
 template <typename T, int G, int D>
 __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, int w_first,
@@ -434,59 +424,44 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
         for (int q = 0; q < cb.NQ; ++q) {
           const half4 h = half4{(_Float16)(cb.acc[q][0] * inv), (_Float16)(cb.acc[q][1] * inv),
                                 (_Float16)(cb.acc[q][2] * inv), (_Float16)(cb.acc[q][3] * inv)};
-          if constexpr (kInKernelMerge) {
-            // written through: the merging workgroup may sit on another XCD
-            uint64_t b;
-            __builtin_memcpy(&b, &h, 8);
-            st_agent64(k.part_o + prow * D + cb.col(q), b);
-          } else {
-            *reinterpret_cast<half4*>(k.part_o + prow * D + cb.col(q)) = h;
-          }
+          // written through: the merging workgroup may sit on another XCD
+          uint64_t b;
+          __builtin_memcpy(&b, &h, 8);
+          st_agent64(k.part_o + prow * D + cb.col(q), b);
         }
         if (cb.cq == 0) {
           const float2 ml = make_float2(cb.M, cb.L);
-          if constexpr (kInKernelMerge) {
-            uint64_t b;
-            __builtin_memcpy(&b, &ml, 8);
-            st_agent64(k.part_ml + prow * 2, b);
-          } else {
-            *reinterpret_cast<float2*>(k.part_ml + prow * 2) = ml;
-          }
+          uint64_t b;
+          __builtin_memcpy(&b, &ml, 8);
+          st_agent64(k.part_ml + prow * 2, b);
         }
       }
     }
 
-    if constexpr (kInKernelMerge) {
-      if (!whole) {
-        // once this workgroup's partial stores have completed, it counts
-        // itself in on the sequence's arrival counter (the last int of its
-        // record); the contributor that brings the count to the number of
-        // contributors merges every partial and puts the counter back to
-        // zero for the next call. No workgroup waits for another.
-        const int w_first = share_owner(g0 + K, C, W);
-        const int w_last = share_owner(g0 + K + n - 1, C, W);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (tid == 0) {
-          int* ctr = reinterpret_cast<int*>(k.recs + v) + 3;
-          const int old = fetch_add_agent(ctr, 1);
-          s_last = old == w_last - w_first;
-          if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          // a dirty counter (start value c != 0) shows a value outside
-          // [0, contributors) to at least one contributor
-          if ((old < 0 || old > w_last - w_first) && a.status)
-            atomicOr(a.status, PKV_STATUS_DIRTY_WORKSPACE);
-        }
-        __syncthreads();
-        if (s_last)
-          merge_cut<T, G, D>(a, k, w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0,
-                             qrow0, tid);
-      }
-    } else if (c0 == 0 && tid == 0) {
-      // contributors of this sequence, for the merge kernel
+    if (!whole) {
+      // once this workgroup's partial stores have completed, it counts
+      // itself in on the sequence's arrival counter (the last int of its
+      // record); the contributor that brings the count to the number of
+      // contributors merges every partial and puts the counter back to
+      // zero for the next call. No workgroup waits for another.
       const int w_first = share_owner(g0 + K, C, W);
       const int w_last = share_owner(g0 + K + n - 1, C, W);
-      k.recs[v] = make_int4(w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0, 0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) {
+        int* ctr = reinterpret_cast<int*>(k.recs + v) + 3;
+        const int old = fetch_add_agent(ctr, 1);
+        s_last = old == w_last - w_first;
+        if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // a dirty counter (start value c != 0) shows a value outside
+        // [0, contributors) to at least one contributor
+        if ((old < 0 || old > w_last - w_first) && a.status)
+          atomicOr(a.status, PKV_STATUS_DIRTY_WORKSPACE);
+      }
+      __syncthreads();
+      if (s_last)
+        merge_cut<T, G, D>(a, k, w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0,
+                           qrow0, tid);
     }
     __syncthreads();  // LDS merge area, table and row buffer are free
     if (!has_next) break;
@@ -500,77 +475,12 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
 }
 
-// Combines the partials of every sequence cut by share boundaries: one
-// thread per (sequence, head, 4 output dims), contributors' loads issued in
-// batches of kMB before any is consumed, running max per head.
-constexpr int kMergeBlock = 256;
-template <typename T, int G, int D>
-__global__ __launch_bounds__(kMergeBlock) void sk_merge_kernel(AttnArgs a, SkArgs k) {
-  const int v = blockIdx.x;
-  // the record and the sequence's metadata in one round trip (scalar loads)
-  const int32_t* rec = reinterpret_cast<const int32_t*>(k.recs) + 4 * (int64_t)v;
-  const int w_first = ld_meta(rec, 0), w_last = ld_meta(rec, 1), r_slot = ld_meta(rec, 2);
-  if (load_desc(a, v, reinterpret_cast<const int32_t*>(k.recs)).n == 0)
-    return;  // no query: nothing was recorded
-  if (w_last <= w_first) return;  // finished in place
-  const int idx = blockIdx.y * kMergeBlock + threadIdx.x;
-  if (idx >= G * D / 4) return;
-  const int head = idx / (D / 4);
-  const int d0 = (idx - head * (D / 4)) * 4;
-  constexpr int kMB = 8;
-  float M = -INFINITY, L = 0.f;
-  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int wb = w_first; wb <= w_last; wb += kMB) {
-    float2 ml[kMB];
-    half4 oo[kMB];
-    // branch-free: contributors past w_last re-read w_last's partial and are
-    // dropped afterwards, so no load sits under a branch (a branch join
-    // would make the compiler wait for every load issued before it)
-#pragma unroll
-    for (int j = 0; j < kMB; ++j) {
-      const int ww = min(wb + j, w_last);
-      const int64_t sl = ww == w_first ? 2 * ww + r_slot : 2 * ww;
-      ml[j] = *reinterpret_cast<const float2*>(k.part_ml + (sl * G + head) * 2);
-      oo[j] = *reinterpret_cast<const half4*>(k.part_o + (sl * G + head) * D + d0);
-    }
-#pragma unroll
-    for (int j = 0; j < kMB; ++j)
-      if (wb + j > w_last) ml[j].x = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kMB; ++j) {
-      if (ml[j].x == -INFINITY) continue;
-      const float Mn = fmaxf(M, ml[j].x);
-      const float sa = exp2f(M - Mn);
-      const float wl = ml[j].y * exp2f(ml[j].x - Mn);  // this partial's weight
-      L = L * sa + wl;
-      acc = acc * sa + floatx4{(float)oo[j][0], (float)oo[j][1], (float)oo[j][2],
-                               (float)oo[j][3]} * wl;
-      M = Mn;
-    }
-  }
-  const int s = v / a.hkv;
-  const int kvh = v - s * a.hkv;
-  const int64_t qrow = (int64_t)(a.qloc ? ld_meta(a.qloc, s) : s) * a.hq + kvh * G + head;
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  T* dst = static_cast<T*>(a.out) + qrow * D + d0;
-  dst[0] = (T)(acc[0] * inv);
-  dst[1] = (T)(acc[1] * inv);
-  dst[2] = (T)(acc[2] * inv);
-  dst[3] = (T)(acc[3] * inv);
-  if (d0 == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
-}
-
 template <typename T, int D, int NT, int PF, bool OFF64>
 int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
   k.n_wg = sk_workgroups(D, 16 * NT);
   hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64>), dim3(k.n_wg), dim3(kBlock), 0,
                      stream, a, k);
-  int rc = check_launch("decode_sk_kernel");
-  if (rc != PKV_OK || kInKernelMerge) return rc;
-  constexpr int G = 16 * NT;
-  const dim3 mgrid(a.n_seq * a.hkv, (G * D / 4 + kMergeBlock - 1) / kMergeBlock);
-  hipLaunchKernelGGL((sk_merge_kernel<T, G, D>), mgrid, dim3(kMergeBlock), 0, stream, a, k);
-  return check_launch("sk_merge_kernel");
+  return check_launch("decode_sk_kernel");
 }
 
 template <typename T, bool OFF64>

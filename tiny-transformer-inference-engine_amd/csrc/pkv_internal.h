@@ -128,15 +128,15 @@ constexpr int kGenRows = 32;
 constexpr int kChunk = 32;  // kv tokens staged per iteration
 
 // Workspace layout: the first kWsCounterBytes are a header. Its first
-// kWsDynCtrBytes hold the dynamic persistent decode kernel's counters (item
-// draws, per-(sequence, kv head) arrivals): they must be zero before the
-// first call on a workspace, and every call leaves them zero. The rest holds
-// the static persistent kernel's per-(sequence, kv head) records (which
-// workgroups hold partials of it), written before they are read in every
-// call. Partials start after the header.
+// kWsCtrBytes hold the partition kernel's per-(sequence, kv head) arrival
+// counters: they must be zero before the first call on a workspace, and
+// every call leaves them zero. The rest holds the persistent kernel's
+// per-(sequence, kv head) records (which workgroups hold partials of it,
+// and an arrival counter with the same zero-in, zero-out rule). Partials
+// start after the header.
 constexpr size_t kWsCounterBytes = 256 * 1024;
-constexpr size_t kWsDynCtrBytes = 8 * 1024;
-constexpr int kMaxCounters = (int)((kWsCounterBytes - kWsDynCtrBytes) / sizeof(int4));
+constexpr size_t kWsCtrBytes = 8 * 1024;
+constexpr int kMaxCounters = (int)((kWsCounterBytes - kWsCtrBytes) / sizeof(int4));
 constexpr int kSkMaxWg = 512;  // workgroups of the persistent kernel, at most
 // A sequence's fixed cost in the persistent kernel (Q load, table slice,
 // wavefront merge, output or partial write) measured in 32-token chunks of
@@ -148,7 +148,7 @@ constexpr int kSkAutoKv = 4096;
 struct SkArgs {
   int n_wg;         // workgroups launched
   int seg_cost;     // overhead of one sequence in chunk units (share balance)
-  int4* recs;       // [n_seq * hkv] (first, last contributor, first's slot)
+  int4* recs;       // [n_seq * hkv] per-pair records: .w is the arrival counter
   _Float16* part_o; // [n_wg][2][G][D] partial outputs, normalised (O / sum)
   float* part_ml;   // [n_wg][2][G][2] partial (max, sum)
 };
@@ -159,29 +159,9 @@ inline size_t sk_workspace_bytes(int group, int d) {
   return kWsCounterBytes + (size_t)kSkMaxWg * 2 * group * ((size_t)d * 2 + 2 * 4);
 }
 
-// Dynamic persistent decode kernel (decode_dyn.hip): one workgroup per CU
-// takes work items (whole short sequences, equal pieces of long ones) from
-// a largest-first list, the first two statically and the rest from an
-// atomic counter.
-constexpr int kDynItemCap = 2048;  // work items per call, at most
-constexpr int kDynMaxSeq = 1024;   // (sequence, kv head) pairs, at most
-constexpr int kDynPiece = 16;      // chunks per piece of a long sequence, at least
-
-struct DynArgs {
-  int piece;          // lower bound of the piece length in chunks
-  int* ctr;           // [0] item counter, [1 + v] arrival counters; zero between calls
-  _Float16* part_o;   // [kDynItemCap][G][D] piece partials, normalised (O / sum)
-  float* part_ml;     // [kDynItemCap][G][2] piece (max, sum)
-};
-
-inline size_t dyn_workspace_bytes(int group, int d) {
-  return kWsCounterBytes + (size_t)kDynItemCap * group * ((size_t)d * 2 + 2 * 4);
-}
-
 struct AttnPlan {
   int kind;        // 0 = generic rows kernel, 1 = MFMA partition kernel,
-                   // 2 = MFMA persistent kernel (static shares), 3 = MFMA
-                   // prefill kernel, 4 = MFMA persistent kernel (dynamic)
+                   // 2 = MFMA persistent kernel, 3 = MFMA prefill kernel
   int rows;        // rows per tile of the chosen kernel
   int part_tokens;
   int parts_max;
@@ -224,9 +204,9 @@ __device__ __forceinline__ int fetch_add_agent(int* p, int x) {
 }
 
 // Counters of the split-K partition kernel's in-kernel merge, one per
-// (sequence, kv head) pair, after the dynamic kernel's in the header.
-constexpr int kMergeCtrOff = 1 + kDynMaxSeq;
-constexpr int kMergeCtrMax = (int)(kWsDynCtrBytes / sizeof(int)) - kMergeCtrOff;
+// (sequence, kv head) pair, at the start of the header.
+constexpr int kMergeCtrOff = 0;
+constexpr int kMergeCtrMax = (int)(kWsCtrBytes / sizeof(int)) - kMergeCtrOff;
 
 __device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
                                           int rows_per_tile, TileGeom& g) {
@@ -303,9 +283,6 @@ int launch_decode_mfma(const AttnArgs& a, const AttnPlan& plan, int dtype,
 // Workgroups the persistent kernel launches for this head shape.
 int sk_workgroups(int d, int group);
 int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream);
-// Dynamic persistent MFMA decode kernel (decode_dyn.hip), same coverage,
-// n_seq * hkv <= kDynMaxSeq.
-int launch_decode_dyn(const AttnArgs& a, const DynArgs& k, int dtype, hipStream_t stream);
 // CUs of the current device (cached; 256 when no device is visible).
 int device_cu_count();
 

@@ -176,13 +176,12 @@ __global__ __launch_bounds__(kSmpThreads) void sample_rows_kernel(
     int* __restrict__ status) {
   __shared__ float key[kSmpCand];
   __shared__ int idx[kSmpCand];
-  __shared__ int s_cnt, s_flags, s_pick;
+  __shared__ int s_cnt, s_flags;
   const int tid = threadIdx.x;
   const T* row = logits + (int64_t)blockIdx.x * row_stride;
   if (tid == 0) {
     s_cnt = 0;
     s_flags = 0;
-    s_pick = 0x7fffffff;
   }
   // 1. thread maxima and finiteness
   // (kSmpUnroll loads of a thread in flight together, indices past the row

@@ -38,7 +38,6 @@ PKV_STATUS_DIRTY_WORKSPACE = 256
 # sequence x kv head pairs and block_size >= 16, else the static one)
 PART_PERSISTENT = -1
 PART_STATIC = -2
-PART_DYNAMIC = -3
 
 _lib = None
 _lock = threading.Lock()
