@@ -234,6 +234,30 @@ int pkv_paged_attention_append(void* out, float* lse, const void* q,
                                int* status, void* stream);
 
 /*
+ * pkv_paged_attention without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): no counterpart in the reference. Same arguments, results and
+ * status bits as pkv_paged_attention; its split-K partials and arrival
+ * counters live in a 16 MiB scratch array the library holds on every device
+ * it runs on, for the life of the process. A problem whose
+ * pkv_attention_workspace_bytes() exceeds 16 MiB returns PKV_ERR_WORKSPACE.
+ * The call allocates nothing (the first call on a device takes the array's
+ * address and zeroes its counter header with a kernel on `stream`). All
+ * calls on one device share that array: calls that overlap on one device
+ * (different streams, or threads) race.
+ */
+int pkv_paged_attention_noalloc(void* out, float* lse, const void* q,
+                                const void* k_pool, const void* v_pool,
+                                int64_t num_blocks, int block_size,
+                                const int32_t* block_tables, int max_blk,
+                                const int32_t* seq_lens,
+                                const int32_t* query_start_loc, int n_seq,
+                                int n_tokens, int max_q_len, int max_kv_len,
+                                int hq, int hkv, int d, float scale, int causal,
+                                int part_tokens, int dtype, int* status,
+                                void* stream);
+
+/*
  * RMSNorm over rows of `dim` elements: y = (x * rsqrt(mean(x^2) + eps)) * w,
  * computed in fp32 and rounded once to `dtype` (weight has `dtype` too).
  * With `delta` non-null, the residual sum r = x + delta (rounded to `dtype`)

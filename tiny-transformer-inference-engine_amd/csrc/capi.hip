@@ -10,6 +10,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "pkv_internal.h"
 
 namespace pkv {
@@ -258,9 +260,82 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
   return launch_attention(ap, sp.pre, dtype, (hipStream_t)stream);
 }
 
+// Scratch of pkv_paged_attention_noalloc: one array per device, in the
+// library's code object (no allocation at call time). Its first
+// kWsCounterBytes are the counter header, which every call leaves at zero;
+// it is cleared once, when a device's address is first taken.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+__global__ void zero_u4_kernel(uint4* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = uint4{0u, 0u, 0u, 0u};
+}
+
+// The current device's scratch address: hipGetSymbolAddress with that device
+// current, once per device (the host-side name `scratch` is not a device
+// address), then the counter header zeroed by a fill kernel on `stream`,
+// ahead of the call's own kernels.
+int scratch_for_current_device(void** ptr, hipStream_t stream) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PKV_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(PKV_ERR_UNSUPPORTED, "device %d beyond the %d the scratch table holds", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(PKV_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    const size_t n = kWsCounterBytes / sizeof(uint4);
+    hipLaunchKernelGGL(zero_u4_kernel, dim3(64), dim3(256), 0, stream,
+                       static_cast<uint4*>(p), n);
+    const int rc = check_launch("zero_u4_kernel");
+    if (rc != PKV_OK) return rc;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return PKV_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int pkv_paged_attention_noalloc(void* out, float* lse, const void* q, const void* k_pool,
+                                const void* v_pool, int64_t num_blocks, int block_size,
+                                const int32_t* block_tables, int max_blk,
+                                const int32_t* seq_lens, const int32_t* query_start_loc,
+                                int n_seq, int n_tokens, int max_q_len, int max_kv_len, int hq,
+                                int hkv, int d, float scale, int causal, int part_tokens,
+                                int dtype, int* status, void* stream) {
+  g_err[0] = 0;
+  if (n_seq > 0 && max_q_len > 0 && hkv > 0 && hq > 0 && hq % hkv == 0 &&
+      part_tokens >= PKV_PART_STATIC) {
+    const size_t need = plan_split(n_seq, max_q_len, hq, hkv, d, max_blk, block_size,
+                                   max_kv_len, part_tokens, dtype, query_start_loc != nullptr)
+                            .ws_bytes;
+    if (need > kScratchBytes)
+      return fail(PKV_ERR_WORKSPACE,
+                  "pkv_paged_attention_noalloc: %zu bytes of scratch needed, the library "
+                  "holds %zu per device; call pkv_paged_attention with a workspace",
+                  need, kScratchBytes);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws, (hipStream_t)stream);
+  if (rc != PKV_OK) return rc;
+  return attention_impl(out, lse, q, k_pool, v_pool, num_blocks, block_size, block_tables,
+                        max_blk, seq_lens, query_start_loc, n_seq, n_tokens, max_q_len,
+                        max_kv_len, hq, hkv, d, scale, causal, part_tokens, dtype, ws,
+                        kScratchBytes, status, stream, nullptr, nullptr, nullptr);
+}
 
 int pkv_paged_attention(void* out, float* lse, const void* q,
                         const void* k_pool, const void* v_pool,

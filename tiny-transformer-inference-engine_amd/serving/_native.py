@@ -71,6 +71,10 @@ _SIGNATURES = {
                                     _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
                                     _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_size,
                                     _c_vp, _c_vp], _c_int),
+    "pkv_paged_attention_noalloc": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int,
+                                     _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int,
+                                     _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
+                                     _c_int, _c_int, _c_vp, _c_vp], _c_int),
     "pkv_rms_norm": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_i64, _c_i64,
                       _c_float, _c_int, _c_vp], _c_int),
     "pkv_rope": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp,
