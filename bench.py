@@ -1,39 +1,52 @@
 """Benchmark of the paged KV-cache decode path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-model] [--no-cpu]
+                    [--no-north-star] [--no-configs]
 
-Workload (the configuration the metric is quoted on):
-bf16 MQA, 12 layers, batch 128 sequences, 16 query heads, 1 KV head,
-head_dim 64, context lengths U[256, 2048] (seed 0), block_size 16, a
+Workload of `value` (the configuration the metric is
+quoted on): bf16 MQA, 12 layers, batch 128 sequences, 16 query heads, 1 KV
+head, head_dim 64, context lengths U[256, 2048] (seed 0), block_size 16, a
 16384-block pool per layer, tables a random permutation of pool blocks.
 One STEP is the path's work for one decode step of that batch: for each of
 the 12 layers, the slot-mapped append of the 128 new K/V rows and the paged
-MQA decode attention over the layer's pool, issued as one library call per
-layer (pkv_paged_attention_append); the same work as two calls per layer is
-reported as value_two_calls. K/V, Q and metadata are resident in HBM before
-timing starts.
+MQA decode attention over that layer's pool, one library call per layer
+(pkv_paged_attention_append). The 12 calls are captured once as a HIP graph
+and the graph is replayed K times between two events (no Python issue cost
+inside the timed region); the same step issued eagerly from Python is
+reported beside it. K/V, Q and metadata are resident in HBM before timing
+starts; the 12 layers' K/V (453 MB) exceed the 256 MB Infinity Cache, so
+each layer is read from HBM.
 
-Printed JSON line:
-  value        algorithmic HBM bytes of the timed steps / their wall time
-               (GB/s), bytes as documented in DESIGN.md (K/V rows read,
-               Q read, O written, block-table entries used, append rows);
-  decode_tok_s full model decode step (dense layers in torch + this path,
-               greedy argmax on device) at batch 128, tokens/s;
-  roofline     the attention kernel alone: bytes per launch / mean launch
-               time from HIP events on its stream, against 8 TB/s;
-  north_star   the same kernel on config 5 (Hq 32, D 128, batch 256,
-               lognormal context mean 1024, fragmented tables);
-  cfg5_mixed_step  config 5's whole step: those 256 decodes plus a
-               chunked-prefill append of 4 new sequences, one fused call;
-  cpu_baseline the reference's PyTorch path (index_select gather + SDPA,
-               the oracle) on this host's cores, on a bounded sample.
+Printed JSON line (one):
+  value          algorithmic HBM bytes of a step / its replay time (GB/s),
+                 bytes as documented in DESIGN.md (K/V rows read, Q read,
+                 O written, block-table entries used, append rows);
+  roofline       the cfg4 attention kernel alone, cold: 12 launches over the
+                 12 layers' pools per graph replay, mean launch time from
+                 events around the replays; the warm figure (one layer
+                 repeated) beside it;
+  north_star     the decode kernel on config 5 (Hq 32, D 128, batch 256,
+                 lognormal context mean 1024, fragmented tables), cold: a
+                 rotation of 5 seeded problems (1.3 GB of pools);
+  cfg5_mixed_step  config 5's whole step (256 decodes + 4 new sequences'
+                 512-token chunked-prefill append, one fused call) at block
+                 sizes 16 and 32, rotated over 3 seeded problems;
+  decode_tok_s   the full config-4 model decode step (projections, this
+                 path, greedy argmax) replayed from one HIP graph;
+  configs        cfg1 (fp32 greedy model step), cfg2 (decode op, fp32 and
+                 bf16), cfg3 (append: 64 x 128-token prefill, 64 ragged
+                 decode rows);
+  cpu_baseline   the reference's PyTorch path restated in oracle/ (gather +
+                 SDPA, index_put append) on this host's cores: a bounded
+                 cfg4 sample in GB/s, and CPU model tok/s for cfg1 and a
+                 cfg4 sample; 3 warm-ups, median of 10.
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
+import statistics
 import sys
 import time
 
@@ -53,7 +66,7 @@ def log(msg):
 
 
 def attn_bytes(lens, hq, hkv, d, esize, bs):
-    """Algorithmic bytes of one decode attention launch (same formula as the
+    """Algorithmic bytes of one decode attention launch (the formula of the
     oracle's decode_attention_bytes, restated so the product bench does not
     depend on the oracle): K+V rows of every visible token, Q in, O out,
     4 B per block-table entry used, 4 B per seq_len."""
@@ -64,9 +77,15 @@ def attn_bytes(lens, hq, hkv, d, esize, bs):
 
 
 def append_bytes(n_tok, hkv, d, esize, n_seq):
-    """K and V rows read and written, plus the int32 metadata the kernel reads
-    (table entry, query_start_loc, start_pos per token, amortised)."""
+    """K and V rows read and written, plus the int32 metadata the fused
+    append reads (table entry, query_start_loc, start_pos; amortised)."""
     return 4 * n_tok * hkv * d * esize + 4 * (n_tok + 2 * n_seq + 1)
+
+
+def write_bytes(n_tok, hkv, d, esize):
+    """KVPool.write with a slot mapping: K and V rows read and written, 8 B
+    per int64 slot."""
+    return 4 * n_tok * hkv * d * esize + 8 * n_tok
 
 
 def time_events(fn, iters, stream):
@@ -81,19 +100,49 @@ def time_events(fn, iters, stream):
     return start.elapsed_time(end) / iters * 1e-3  # seconds per call
 
 
+class Graph:
+    """`fn` captured once as a HIP graph, with a private library workspace
+    (kept for the graph's lifetime). Warmed up eagerly on a side stream
+    first (workspace and allocator pools are created there)."""
+
+    def __init__(self, fn, warmup=2):
+        import torch
+        from serving import _native
+        self.ws = _native.Workspace()
+        dev = torch.device("cuda:0")
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with _native.workspace_scope(self.ws):
+            with torch.cuda.stream(side), torch.no_grad():
+                for _ in range(max(1, warmup)):
+                    fn()
+            torch.cuda.current_stream(dev).wait_stream(side)
+            torch.cuda.synchronize(dev)
+            self.g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.g), torch.no_grad():
+                fn()
+        torch.cuda.synchronize(dev)
+
+    def replay(self):
+        self.g.replay()
+
+    def time(self, replays, warm=3):
+        import torch
+        for _ in range(warm):
+            self.g.replay()
+        return time_events(self.g.replay, replays, torch.cuda.current_stream())
+
+
 def cfg4_tables(lens, bs, num_blocks, extra_tokens, seed):
     from serving import workloads
     return workloads.permuted_tables([int(x) + extra_tokens for x in lens], bs, num_blocks, seed)
 
 
-def run_hot_path(args, torch):
-    """Config-4 hot path: 12 x (append + paged decode attention), one
-    library call per layer (pkv_paged_attention_append: the append fused
-    into the attention launch). The same step as two calls per layer
-    (KVPool.write_from_table + paged_attention_meta, the reference's
-    serving/paged_mqa.py:98-110 structure) is timed beside it."""
+def build_cfg4_path(torch):
+    """Config 4's path state: a 12-layer pool (each layer N(0,1)), the
+    step's metadata (each sequence appends at position lens[i] and attends
+    over lens[i] + 1 keys), Q and the new K/V rows."""
     from serving import workloads
-    from serving.fake_paged_attn import paged_attention_append_meta, paged_attention_meta
     from serving.kv_pool import KVPool
     from serving.paged_meta import pack_batch_meta
 
@@ -105,15 +154,24 @@ def run_hot_path(args, torch):
     g = torch.Generator(device=dev).manual_seed(0)
     for l in range(L):
         pool.kv[l].normal_(generator=g)
-    # the step appends each sequence's token at position lens[i] and attends
-    # over lens[i] + 1 keys
-    pos = [int(x) for x in lens]
-    meta = pack_batch_meta(tables, list(range(N + 1)), pos, N, dev, BS)
+    meta = pack_batch_meta(tables, list(range(N + 1)), [int(x) for x in lens], N, dev, BS)
     q = torch.randn(N, HQ, D, generator=g, device=dev).bfloat16()
     knew = torch.randn(N, HKV, D, generator=g, device=dev).bfloat16()
     vnew = torch.randn(N, HKV, D, generator=g, device=dev).bfloat16()
+    return dict(L=L, N=N, HQ=HQ, HKV=HKV, D=D, BS=BS, lens=lens, tables=tables, pool=pool,
+                meta=meta, q=q, knew=knew, vnew=vnew)
+
+
+def run_hot_path(args, torch, st):
+    """The value step: 12 x (append + attention), one call per layer, from
+    a HIP graph; the same step issued eagerly, and as two calls per layer
+    (KVPool.write_from_table + paged_attention_meta, the reference's
+    serving/paged_mqa.py:98-110 structure), beside it."""
+    from serving.fake_paged_attn import paged_attention_append_meta, paged_attention_meta
+
+    L, pool, meta, q, knew, vnew = st["L"], st["pool"], st["meta"], st["q"], st["knew"], st["vnew"]
     out = torch.empty_like(q)
-    stream = torch.cuda.current_stream(dev)
+    stream = torch.cuda.current_stream()
 
     def step():
         for l in range(L):
@@ -124,43 +182,142 @@ def run_hot_path(args, torch):
             pool.write_from_table(l, knew, vnew, meta)
             paged_attention_meta(q, pool.kv[l, 0], pool.kv[l, 1], meta, out=out)
 
-    kv_after = lens + 1
-    per_layer_attn = attn_bytes(kv_after, HQ, HKV, D, 2, BS)
-    per_layer_app = append_bytes(N, HKV, D, 2, N)
+    kv_after = st["lens"] + 1
+    per_layer_attn = attn_bytes(kv_after, st["HQ"], st["HKV"], st["D"], 2, st["BS"])
+    per_layer_app = append_bytes(st["N"], st["HKV"], st["D"], 2, st["N"])
     step_bytes = L * (per_layer_attn + per_layer_app)
 
+    graph = Graph(step, warmup=args.warmup)
+    sec = graph.time(args.steps)
+    log(f"hot path (HIP graph): {sec * 1e6:.1f} us/step, {step_bytes / sec / 1e9:.0f} GB/s")
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    sec = time_events(step, args.steps, stream)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
-    log(f"hot path: {sec * 1e6:.1f} us/step (events), {wall * 1e6:.1f} us/step (wall)")
+    eager = time_events(step, args.steps, stream)
+    log(f"hot path (eager calls): {eager * 1e6:.1f} us/step")
     for _ in range(args.warmup):
         step_two_calls()
-    sec2 = time_events(step_two_calls, args.steps, stream)
-    log(f"hot path as append + attention calls: {sec2 * 1e6:.1f} us/step")
+    two = time_events(step_two_calls, args.steps, stream)
+    log(f"hot path as append + attention calls (eager): {two * 1e6:.1f} us/step")
+    return dict(step_sec=sec, eager_sec=eager, two_calls_sec=two, step_bytes=step_bytes,
+                attn_bytes=per_layer_attn)
 
-    # the dominant kernel alone: attention on layer 0, back to back
-    def attn():
-        paged_attention_meta(q, pool.kv[0, 0], pool.kv[0, 1], meta, out=out)
-    for _ in range(5):
-        attn()
-    a_sec = time_events(attn, 200, stream)
-    log(f"attention alone: {a_sec * 1e6:.2f} us/launch, {per_layer_attn / 1e6:.2f} MB")
-    return dict(step_sec=sec, wall_sec=wall, step_bytes=step_bytes, step_sec_two_calls=sec2,
-                attn_sec=a_sec, attn_bytes=per_layer_attn, lens=lens, tables=tables,
-                pool=pool, q=q, meta=meta)
+
+def run_roofline_cfg4(args, torch, st):
+    """The cfg4 decode attention kernel alone (decode_mfma_kernel): cold,
+    12 launches over the 12 layers' pools per graph replay (each layer's
+    39 MB of K/V last read 11 launches = 430 MB earlier, beyond the 256 MB
+    Infinity Cache); warm, 12 launches over layer 0."""
+    from serving.fake_paged_attn import paged_attention_meta
+
+    L, pool, meta, q = st["L"], st["pool"], st["meta"], st["q"]
+    out = torch.empty_like(q)
+    cold = Graph(lambda: [paged_attention_meta(q, pool.kv[l, 0], pool.kv[l, 1], meta, out=out)
+                          for l in range(L)])
+    warm = Graph(lambda: [paged_attention_meta(q, pool.kv[0, 0], pool.kv[0, 1], meta, out=out)
+                          for _ in range(L)])
+    reps = max(10, args.steps)
+    c = cold.time(reps) / L
+    w = warm.time(reps) / L
+    nbytes = attn_bytes(st["lens"] + 1, st["HQ"], st["HKV"], st["D"], 2, st["BS"])
+    log(f"cfg4 attention: cold {c * 1e6:.2f} us ({nbytes / c / 1e9:.0f} GB/s), "
+        f"warm {w * 1e6:.2f} us ({nbytes / w / 1e9:.0f} GB/s)")
+    return dict(cold_sec=c, warm_sec=w, bytes=nbytes)
+
+
+def run_north_star(args, torch):
+    """Config 5 decode attention (bs 16): cold over a rotation of 5 seeded
+    problems (each 136 MB of K/V in a 268 MB pool), warm on seed 0."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_mqa_decode
+
+    dev = torch.device("cuda:0")
+    probs = [workloads.cfg5_problem(dev, seed=s, bs=16) for s in range(5)]
+    outs = [torch.empty_like(p.q) for p in probs]
+
+    def launch(i):
+        p = probs[i]
+        paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens,
+                         max_kv_len=int(p.lens.max()), out=outs[i])
+    cold = Graph(lambda: [launch(i) for i in range(len(probs))])
+    warm = Graph(lambda: [launch(0) for _ in range(len(probs))])
+    reps = max(10, args.steps)
+    c = cold.time(reps) / len(probs)
+    w = warm.time(reps) / len(probs)
+    nb = [attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs) for p in probs]
+    c_gbs = sum(nb) / len(nb) / c / 1e9
+    w_gbs = nb[0] / w / 1e9
+    log(f"cfg5 attention: cold {c * 1e6:.2f} us ({c_gbs:.0f} GB/s, {100 * c_gbs / HBM_PEAK_GBS:.1f}%),"
+        f" warm {w * 1e6:.2f} us ({w_gbs:.0f} GB/s)")
+    res = {"workload": "cfg5 paged MQA decode attention: batch 256, Hq 32, Hkv 1, D 128, bf16, "
+                       "lognormal ctx mean 1024 cap 8192, bs 16, fragmented tables; cold = a "
+                       "graph replaying one launch on each of 5 seeded problems (seeds 0-4, "
+                       "1.3 GB of pools), warm = 5 launches on seed 0",
+           "kernel": "decode_sk_kernel (persistent, equal shares of all context chunks)",
+           "us_per_launch": round(c * 1e6, 3), "bytes_per_launch": int(sum(nb) / len(nb)),
+           "achieved_gbs": round(c_gbs, 1), "frac_of_peak": round(c_gbs / HBM_PEAK_GBS, 4),
+           "warm_us_per_launch": round(w * 1e6, 3), "warm_bytes_per_launch": nb[0],
+           "warm_achieved_gbs": round(w_gbs, 1), "target_frac": 0.70}
+    del probs, outs, cold, warm
+    torch.cuda.empty_cache()
+    return res
+
+
+def mixed_step_bytes(dec_lens, chunk, n_new, hq=32, d=128, esize=2, bs=16):
+    """Algorithmic bytes of one config-5 mixed step: every visible K/V row
+    read once (decode contexts after the append, each new sequence's chunk),
+    Q in and O out for every query token, the appended K/V rows read and
+    written, 4 B per block-table entry used and per seq_len."""
+    dec_kv = [int(x) + 1 for x in dec_lens]
+    kv = sum(dec_kv) + n_new * chunk
+    T = len(dec_kv) + n_new * chunk
+    blocks = sum((x + bs - 1) // bs for x in dec_kv) + n_new * ((chunk + bs - 1) // bs)
+    return (kv * d * 2 * esize + 2 * T * hq * d * esize + 4 * T * d * esize
+            + 4 * blocks + 4 * (len(dec_kv) + n_new))
+
+
+def run_mixed_step(args, torch):
+    """Config 5's step as BASELINE defines it: the 256 decode queries and a
+    512-token chunked-prefill append for 4 new sequences (4 x 128 also
+    reported at bs 16), one fused append + attention call, block sizes 16
+    and 32; each graph replay runs the step on 3 seeded problems."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_attention_append_meta
+
+    dev = torch.device("cuda:0")
+    res = {}
+    for bs, chunk in ((16, 512), (32, 512), (16, 128)):
+        probs = [workloads.cfg5_mixed_problem(dev, chunk=chunk, seed=s, bs=bs) for s in range(3)]
+        outs = [torch.empty_like(p.q) for p in probs]
+
+        def step(i):
+            p = probs[i]
+            paged_attention_append_meta(p.q, p.k, p.v, p.pool, 0, p.meta, out=outs[i])
+        graph = Graph(lambda: [step(i) for i in range(len(probs))])
+        sec = graph.time(max(10, args.steps)) / len(probs)
+        nbytes = sum(mixed_step_bytes(p.dec_lens, chunk, p.n_new, bs=bs) for p in probs) / len(probs)
+        gbs = nbytes / sec / 1e9
+        log(f"cfg5 mixed step bs {bs} (256 decode + 4 x {chunk} prefill): {sec * 1e6:.1f} us, "
+            f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
+        res[f"bs{bs}_prefill{chunk}"] = {"us_per_step": round(sec * 1e6, 2),
+                                         "bytes_per_step": int(nbytes),
+                                         "achieved_gbs": round(gbs, 1),
+                                         "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        del probs, outs, graph
+        torch.cuda.empty_cache()
+    res["workload"] = ("cfg5 step: 256 decode queries (lognormal ctx mean 1024 cap 8192) each "
+                       "appending one token, plus a chunked-prefill append of 4 new sequences "
+                       "(4 x 512; 4 x 128 at bs 16), bf16, Hq 32, Hkv 1, D 128, fragmented "
+                       "tables; one fused append + attention call; a graph replays the step on "
+                       "3 seeded problems (cold)")
+    return res
 
 
 def run_model(args, torch):
     """Full bf16 model decode step at batch 128 (config 4), tokens/s."""
-    from serving import workloads
+    from serving import fused_ops, workloads
     from serving.kv_pool import KVPool
     from serving.layers import ModelConfig
     from serving.paged_meta import pack_batch_meta
-    from serving import fused_ops
     from serving.paged_model import PagedTransformer
 
     dev = torch.device("cuda:0")
@@ -169,7 +326,7 @@ def run_model(args, torch):
                       num_kv_heads=1, max_seq_len=4096)
     torch.manual_seed(0)
     model = PagedTransformer(cfg).to(dev, torch.bfloat16).eval()
-    N, BS, NB = 128, 16, 16384
+    N, BS, NB = N_MODEL, 16, 16384
     lens = workloads.lengths_uniform(N, 256, 2048, seed=0)
     tables = cfg4_tables(lens, BS, NB, 2 * steps + args.warmup + 8, seed=0)
     pool = KVPool(cfg.num_layers, BS, NB, 1, cfg.head_dim, torch.bfloat16, dev)
@@ -198,7 +355,6 @@ def run_model(args, torch):
         torch.cuda.synchronize()
         eager = time_events(step, max(steps // 3, 3), stream)
     log(f"model decode step, eager launches: {eager * 1e3:.3f} ms, {N / eager:.0f} tok/s")
-    # the same step captured once as a HIP graph and replayed
     from serving.graph_step import DecodeStepGraph
     graph = DecodeStepGraph(model, pool, meta, ids, warmup=1)
     for _ in range(args.warmup):
@@ -206,134 +362,253 @@ def run_model(args, torch):
     torch.cuda.synchronize()
     sec = time_events(graph.replay, steps, stream)
     log(f"model decode step, HIP graph: {sec * 1e3:.3f} ms, {N / sec:.0f} tok/s")
-    return dict(step_sec=sec, tok_s=N / sec, eager_step_sec=eager)
+    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    del graph, pool, model
+    torch.cuda.empty_cache()
+    return dict(step_sec=sec, tok_s=N / sec, eager_step_sec=eager, state_dict=sd, cfg=cfg,
+                lens=lens)
 
 
-def run_north_star(args, torch):
-    """Config 5 attention kernel alone (bs 16): achieved GB/s."""
-    from serving import workloads
-    from serving.fake_paged_attn import paged_mqa_decode
-
-    dev = torch.device("cuda:0")
-    p = workloads.cfg5_problem(dev, seed=0, bs=16)
-    out = torch.empty_like(p.q)
-    mk = int(p.lens.max())
-
-    def attn():
-        paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens,
-                         max_kv_len=mk, out=out)
-    for _ in range(5):
-        attn()
-    sec = time_events(attn, 100, torch.cuda.current_stream(dev))
-    nbytes = attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs)
-    gbs = nbytes / sec / 1e9
-    log(f"cfg5 attention: {sec * 1e6:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
-    return {"workload": "cfg5 paged MQA decode attention: batch 256, Hq 32, Hkv 1, D 128, bf16, "
-                        "lognormal ctx mean 1024 cap 8192 (seed 0), bs 16, fragmented tables",
-            "sum_kv": int(p.lens.sum()), "us_per_launch": sec * 1e6,
-            "bytes_per_launch": nbytes, "achieved_gbs": gbs,
-            "frac_of_peak": gbs / HBM_PEAK_GBS, "target_frac": 0.70}
+def cfg1_model(torch, dev):
+    from serving.layers import ModelConfig
+    from serving.paged_model import PagedTransformer
+    cfg = ModelConfig(vocab_size=50257, d_model=128, num_layers=4, num_heads=4,
+                      num_kv_heads=1, max_seq_len=128)
+    torch.manual_seed(0)
+    return cfg, PagedTransformer(cfg).to(dev).eval()
 
 
-def mixed_step_bytes(dec_lens, chunk, n_new, hq=32, d=128, esize=2, bs=16):
-    """Algorithmic bytes of one config-5 mixed step: every visible K/V row
-    read once (decode contexts after the append, each new sequence's chunk),
-    Q in and O out for every query token, the appended K/V rows read and
-    written, 4 B per block-table entry used and per seq_len."""
-    dec_kv = [int(x) + 1 for x in dec_lens]
-    kv = sum(dec_kv) + n_new * chunk
-    T = len(dec_kv) + n_new * chunk
-    blocks = sum((x + bs - 1) // bs for x in dec_kv) + n_new * ((chunk + bs - 1) // bs)
-    return (kv * d * 2 * esize + 2 * T * hq * d * esize + 4 * T * d * esize
-            + 4 * blocks + 4 * (len(dec_kv) + n_new))
-
-
-def run_mixed_step(args, torch):
-    """Config 5 as BASELINE defines its step: the 256 decode queries and a
-    chunked-prefill append for 4 new sequences (4 x 128 tokens; 4 x 512 also
-    reported), one fused append + attention call (bs 16)."""
-    from serving import workloads
-    from serving.fake_paged_attn import paged_attention_append_meta
-
-    dev = torch.device("cuda:0")
-    res = {}
-    for chunk in (128, 512):
-        p = workloads.cfg5_mixed_problem(dev, chunk=chunk, seed=0, bs=16)
-        out = torch.empty_like(p.q)
-
-        def step():
-            paged_attention_append_meta(p.q, p.k, p.v, p.pool, 0, p.meta, out=out)
-        for _ in range(5):
-            step()
-        sec = time_events(step, 50, torch.cuda.current_stream(dev))
-        nbytes = mixed_step_bytes(p.dec_lens, chunk, p.n_new)
-        gbs = nbytes / sec / 1e9
-        log(f"cfg5 mixed step (256 decode + 4 x {chunk} prefill): {sec * 1e6:.1f} us, "
-            f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
-        res[f"prefill_{chunk}"] = {"us_per_step": round(sec * 1e6, 2), "bytes_per_step": nbytes,
-                                   "achieved_gbs": round(gbs, 1),
-                                   "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
-    res["workload"] = ("cfg5 step: 256 decode queries (lognormal ctx mean 1024 cap 8192, seed 0) "
-                       "each appending one token, plus a chunked-prefill append of 4 new "
-                       "sequences (4 x 128, and 4 x 512), bf16, Hq 32, Hkv 1, D 128, bs 16, "
-                       "fragmented tables; one fused append + attention call")
-    return res
-
-
-def run_cpu_baseline(hot, torch):
-    """The reference's PyTorch paged path (oracle.torch_ref: per-sequence
-    index_select gather + scaled_dot_product_attention, as in the
-    reference's tests/test.py:145-178) on the host CPU, bf16 as in the GPU
-    workload, over a bounded sample: one layer, the first 16 sequences of
-    the config-4 batch, repeated for about 10 s."""
-    from oracle import torch_ref
-
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    pool = hot["pool"]
-    kp = pool.kv[0, 0].cpu()
-    vp = pool.kv[0, 1].cpu()
-    q = hot["q"][:16].cpu()
-    lens = [int(x) + 1 for x in hot["lens"][:16]]
-    tables = hot["tables"][:16]
-    nbytes = attn_bytes(lens, q.shape[1], 1, q.shape[2], 2, pool.block_size)
-    for _ in range(2):
-        torch_ref.paged_attention_sdpa(q, kp, vp, tables, lens)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        torch_ref.paged_attention_sdpa(q, kp, vp, tables, lens)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 2000:
-            break
-    sec = el / reps
-    gbs = nbytes / sec / 1e9
-    log(f"cpu baseline: {sec * 1e3:.2f} ms per sample, {gbs:.3f} GB/s on {threads} threads")
-    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"1 layer, 16 of the 128 config-4 sequences (sum kv {sum(lens)}), bf16, "
-                      f"{reps} repetitions over {el:.1f} s; torch gather + SDPA "
-                      "(oracle/torch_ref.paged_attention_sdpa)"}
-
-
-def run_profile(args, torch):
-    """Profiling target: only the decode-attention launches of one workload
-    (no timing, no JSON), optionally followed by a plain device copy of
-    known size, the reference for scaling HBM counters."""
-    from serving import workloads
-    from serving.fake_paged_attn import paged_attention_meta, paged_mqa_decode
+def run_cfg1(args, torch):
+    """Config 1 on the GPU: the fp32 reference-size model, 2 sequences of
+    16-token prompts, greedy decode; the decode step (2 tokens) replayed
+    from its HIP graph, 79 steps (80 tokens per sequence with the prefill's)."""
+    from serving.allocator import BlockAllocator
+    from serving.graph_step import DecodeStepGraph
     from serving.kv_pool import KVPool
     from serving.paged_meta import pack_batch_meta
 
     dev = torch.device("cuda:0")
+    cfg, model = cfg1_model(torch, dev)
+    BS, NB, P, NEW = 16, 256, 16, 80
+    alloc = BlockAllocator(NB)
+    tables = [alloc.allocate_n((P + NEW + BS - 1) // BS) for _ in range(2)]
+    pool = KVPool(cfg.num_layers, BS, NB, 1, cfg.head_dim, torch.float32, dev)
+    g = torch.Generator().manual_seed(0)
+    prompts = torch.randint(0, cfg.vocab_size, (2, P), generator=g)
+    pre = pack_batch_meta(tables, [0, P, 2 * P], list(range(P)) * 2, 2 * P, dev, BS)
+    with torch.no_grad():
+        logits = model.forward_step(prompts.reshape(-1).to(dev), pool, pre)
+    ids = logits.argmax(-1)
+    meta = pack_batch_meta(tables, [0, 1, 2], [P, P], 2, dev, BS)
+    meta.max_kv_len = P + NEW
+    graph = DecodeStepGraph(model, pool, meta, ids, warmup=1)
+    steps = NEW - 2  # the warm-up step is the first decode step
+    sec = time_events(graph.replay, steps, torch.cuda.current_stream(dev))
+    log(f"cfg1 fp32 greedy decode step (2 sequences): {sec * 1e6:.1f} us, {2 / sec:.0f} tok/s")
+    return {"workload": "cfg1: fp32 model d_model 128, 4 layers, Hq 4, Hkv 1, D 32, vocab 50257, "
+                        "2 sequences x 16-token prompts, 80 greedy tokens, bs 16, 256 blocks; "
+                        "decode step from its HIP graph",
+            "us_per_step": round(sec * 1e6, 2), "tok_s": round(2 / sec, 1)}
+
+
+def run_cfg2(args, torch):
+    """Config 2: the isolated decode op (batch 32, Hq 8, Hkv 1, D 32, bs 16,
+    1024-block pool, contexts U[64, 256]) in fp32 and bf16; 50 launches per
+    graph replay (0.7-1.4 MB: cache resident, launch-latency bound)."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_mqa_decode
+
+    dev = torch.device("cuda:0")
+    res = {}
+    for dt, name, es in ((torch.float32, "fp32", 4), (torch.bfloat16, "bf16", 2)):
+        p = workloads.cfg2_problem(dt, dev, seed=0)
+        out = torch.empty_like(p.q)
+        mk = int(p.lens.max())
+        graph = Graph(lambda: [paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables,
+                                                p.seq_lens, max_kv_len=mk, out=out)
+                               for _ in range(50)])
+        sec = graph.time(20) / 50
+        nb = attn_bytes(p.lens, p.hq, p.hkv, p.d, es, p.bs)
+        log(f"cfg2 decode op {name}: {sec * 1e6:.2f} us, {nb / sec / 1e9:.0f} GB/s")
+        res[name] = {"us_per_op": round(sec * 1e6, 3), "bytes": nb,
+                     "achieved_gbs": round(nb / sec / 1e9, 1)}
+    res["workload"] = ("cfg2 decode op: batch 32, Hq 8, Hkv 1, D 32, bs 16, 1024-block pool, "
+                       "ctx U[64,256], permuted tables; 50 launches per graph replay")
+    return res
+
+
+def run_cfg3(args, torch):
+    """Config 3: KVPool.write of a 64 x 128-token prefill (one slot mapping
+    over the whole batch) and of 64 single-token decode rows at ragged
+    positions, bf16, D 64, 4096-block pool, blocks from a shuffled free
+    list; each timed from a graph replaying the write 20 times."""
+    import numpy as np
+    from serving.allocator import BlockAllocator
+    from serving.kv_pool import KVPool
+
+    dev = torch.device("cuda:0")
+    NB, BS, D = 4096, 16, 64
+    alloc = BlockAllocator(NB)
+    rng = np.random.default_rng(0)
+    ids = alloc.allocate_n(alloc.num_free)
+    alloc.free([int(x) for x in rng.permutation(ids)])
+    tables = [alloc.allocate_n(9) for _ in range(64)]  # 128 prompt + room to grow
+    pool = KVPool(1, BS, NB, 1, D, torch.bfloat16, dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    slots = torch.cat([pool.make_slot_mapping(0, 128, t) for t in tables])
+    k = torch.randn(64 * 128, 1, D, generator=g, device=dev).bfloat16()
+    v = torch.randn(64 * 128, 1, D, generator=g, device=dev).bfloat16()
+    pos = [128 + int(x) for x in rng.integers(0, 16, size=64)]
+    dslots = torch.cat([pool.make_slot_mapping(p, 1, t) for p, t in zip(pos, tables)])
+    dk = torch.randn(64, 1, D, generator=g, device=dev).bfloat16()
+    dv = torch.randn(64, 1, D, generator=g, device=dev).bfloat16()
+    res = {}
+    for name, sl, kk, vv in (("prefill", slots, k, v), ("decode", dslots, dk, dv)):
+        graph = Graph(lambda: [pool.write(0, sl, kk, vv) for _ in range(20)])
+        sec = graph.time(20) / 20
+        nb = write_bytes(sl.numel(), 1, D, 2)
+        log(f"cfg3 {name} append ({sl.numel()} rows): {sec * 1e6:.2f} us, {nb / sec / 1e9:.0f} GB/s")
+        res[name] = {"rows": int(sl.numel()), "us_per_write": round(sec * 1e6, 3), "bytes": nb,
+                     "achieved_gbs": round(nb / sec / 1e9, 1)}
+    res["workload"] = ("cfg3 append: 64 x 128-token prefill write and 64 ragged single-token "
+                       "decode rows, bf16, Hkv 1, D 64, bs 16, 4096 blocks from a shuffled free "
+                       "list; 20 writes per graph replay")
+    return res
+
+
+def cpu_threads():
+    n = os.environ.get("OMP_NUM_THREADS")
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(int(n), avail)) if n and n.isdigit() else avail
+
+
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def median_time(fn, warm=3, reps=10):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def run_cpu_baseline(st, model, torch):
+    """The reference's PyTorch paged path as restated in oracle/torch_ref
+    (index_put append, per-sequence index_select gather + SDPA with the
+    bottom-right causal mask, tests/test.py:145-178) on this host's cores,
+    3 warm-ups then the median of 10:
+      - value: one layer of the cfg4 path step for 16 of the 128 sequences
+        (their 16 appends + attention), bf16 as on the GPU, in GB/s;
+      - cfg1 model: the fp32 model's greedy decode step for its 2 sequences;
+      - cfg4 model: the bf16 model's weights in fp32, one decode step for
+        16 of the 128 sequences (contexts of their lengths, random K/V)."""
+    from oracle import torch_ref
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    # cfg4 path sample
+    pool = st["pool"]
+    S = 16
+    kp = pool.kv[0, 0].cpu().clone()
+    vp = pool.kv[0, 1].cpu().clone()
+    q = st["q"][:S].cpu()
+    kn, vn = st["knew"][:S].cpu(), st["vnew"][:S].cpu()
+    lens = [int(x) + 1 for x in st["lens"][:S]]
+    tables = st["tables"][:S]
+    bs = pool.block_size
+    slots = torch.tensor([tables[i][(lens[i] - 1) // bs] * bs + (lens[i] - 1) % bs
+                          for i in range(S)], dtype=torch.long)
+    fk, fv = kp.view(-1, 1, st["D"]), vp.view(-1, 1, st["D"])
+
+    def path():
+        torch_ref.append_index_put(fk, fv, slots, kn, vn)
+        torch_ref.paged_attention_sdpa(q, kp, vp, tables, lens)
+    sec = median_time(path)
+    nbytes = attn_bytes(lens, q.shape[1], 1, q.shape[2], 2, bs) + append_bytes(S, 1, st["D"], 2, S)
+    gbs = nbytes / sec / 1e9
+    log(f"cpu baseline (cfg4 path, 1 layer x {S} seqs): {sec * 1e3:.2f} ms, {gbs:.3f} GB/s, "
+        f"{threads} threads")
+    res = {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+           "cpu_model": cpu_model_name(),
+           "sample": f"cfg4 path, 1 layer: append + attention for 16 of the 128 sequences "
+                     f"(sum kv {sum(lens)}), bf16; oracle/torch_ref (index_put + gather + SDPA); "
+                     f"3 warm-ups, median of 10 ({sec * 1e3:.2f} ms each)"}
+    # cfg1 model on the CPU
+    cfg1, m1 = cfg1_model(torch, torch.device("cpu"))
+    sd1 = {k: v.detach() for k, v in m1.state_dict().items()}
+    ref1 = torch_ref.RefModel(sd1, cfg1.num_layers, cfg1.num_heads, cfg1.num_kv_heads,
+                              cfg1.max_seq_len)
+    g = torch.Generator().manual_seed(0)
+    prompts = torch.randint(0, cfg1.vocab_size, (2, 16), generator=g)
+    toks = [int(ref1.forward_seq(i, prompts[i].tolist(), list(range(16))).argmax())
+            for i in range(2)]
+    pos = [16, 16]
+
+    def step1():
+        for i in range(2):
+            toks[i] = int(ref1.forward_seq(i, [toks[i]], [pos[i]]).argmax())
+            pos[i] += 1
+    with torch.no_grad():
+        s1 = median_time(step1)
+    res["cfg1_model_tok_s"] = round(2 / s1, 1)
+    res["cfg1_sample"] = "fp32 decode step of both sequences (positions 16-29), median of 10"
+    log(f"cpu cfg1 model: {s1 * 1e3:.2f} ms/step, {2 / s1:.0f} tok/s")
+    # cfg4 model sample on the CPU
+    if model is not None:
+        cfg = model["cfg"]
+        ref4 = torch_ref.RefModel(model["state_dict"], cfg.num_layers, cfg.num_heads,
+                                  cfg.num_kv_heads, cfg.max_seq_len)
+        gk = torch.Generator().manual_seed(2)
+        ctx = [int(x) for x in model["lens"][:S]]
+        for i, n in enumerate(ctx):
+            ref4.cache[i] = [[torch.randn(n, 1, cfg.head_dim, generator=gk),
+                              torch.randn(n, 1, cfg.head_dim, generator=gk)]
+                             for _ in range(cfg.num_layers)]
+        tok4 = [1] * S
+
+        def step4():
+            for i in range(S):
+                tok4[i] = int(ref4.forward_seq(i, [tok4[i]], [ctx[i]]).argmax())
+                ctx[i] += 1
+        with torch.no_grad():
+            s4 = median_time(step4)
+        res["cfg4_model_tok_s"] = round(S / s4, 1)
+        res["cfg4_sample"] = (f"fp32 decode step of 16 of the 128 cfg4 sequences (their context "
+                              f"lengths, random K/V), median of 10 ({s4 * 1e3:.1f} ms each)")
+        log(f"cpu cfg4 model sample: {s4 * 1e3:.1f} ms/step for {S} seqs, {S / s4:.1f} tok/s")
+    return res
+
+
+def run_profile(args, torch):
+    """Profiling target: only the launches of one workload, as the bench
+    times them (no timing, no JSON), optionally followed by an elementwise
+    kernel over a buffer of known size, the reference for scaling HBM
+    counters."""
+    from serving import workloads
+    from serving.fake_paged_attn import paged_attention_append_meta, paged_mqa_decode
+
+    dev = torch.device("cuda:0")
     if args.profile == "model":
-        # the config-4 model decode step, replayed from its HIP graph
         args.model_steps = args.profile_iters
         args.warmup = 1
         run_model(args, torch)
         return
     if args.profile == "sampling":
-        # the scheduler's sampling step at config 4's batch: 128 rows of a
-        # 50257-entry bf16 vocabulary, top_k 32, top_p 0.9, temperature 1
         from serving import fused_ops
         g = torch.Generator(device=dev).manual_seed(0)
         logits = torch.randn(128, 50257, generator=g, device=dev).bfloat16()
@@ -343,39 +618,37 @@ def run_profile(args, torch):
         torch.cuda.synchronize()
         log(f"profile sampling: {args.profile_iters} launches")
         return
-    if args.profile == "cfg5mixed":
-        p = workloads.cfg5_mixed_problem(dev, chunk=128, seed=0, bs=16)
-        out = torch.empty_like(p.q)
-        from serving.fake_paged_attn import paged_attention_append_meta
-
-        def attn():
-            paged_attention_append_meta(p.q, p.k, p.v, p.pool, 0, p.meta, out=out)
-        nbytes = mixed_step_bytes(p.dec_lens, 128, p.n_new)
-    elif args.profile == "cfg4":
-        L, N, HQ, HKV, D, BS, NB = 1, 128, 16, 1, 64, 16, 16384
-        lens = workloads.lengths_uniform(N, 256, 2048, seed=0)
-        tables = cfg4_tables(lens, BS, NB, 1, seed=0)
-        pool = KVPool(L, BS, NB, HKV, D, torch.bfloat16, dev)
-        g = torch.Generator(device=dev).manual_seed(0)
-        pool.kv[0].normal_(generator=g)
-        meta = pack_batch_meta(tables, list(range(N + 1)), [int(x) for x in lens], N, dev, BS)
-        q = torch.randn(N, HQ, D, generator=g, device=dev).bfloat16()
-        out = torch.empty_like(q)
-
-        def attn():
-            paged_attention_meta(q, pool.kv[0, 0], pool.kv[0, 1], meta, out=out)
-        nbytes = attn_bytes(lens + 1, HQ, HKV, D, 2, BS)
+    if args.profile == "cfg4":
+        # the roofline's cold rotation: every layer's pool in turn
+        from serving.fake_paged_attn import paged_attention_meta
+        st = build_cfg4_path(torch)
+        out = torch.empty_like(st["q"])
+        graph = Graph(lambda: [paged_attention_meta(st["q"], st["pool"].kv[l, 0],
+                                                    st["pool"].kv[l, 1], st["meta"], out=out)
+                               for l in range(st["L"])])
+        n_per = st["L"]
+    elif args.profile == "cfg4step":
+        st = build_cfg4_path(torch)
+        out = torch.empty_like(st["q"])
+        graph = Graph(lambda: [paged_attention_append_meta(st["q"], st["knew"], st["vnew"],
+                                                           st["pool"], l, st["meta"], out=out)
+                               for l in range(st["L"])])
+        n_per = st["L"]
+    elif args.profile == "cfg5mixed":
+        probs = [workloads.cfg5_mixed_problem(dev, chunk=512, seed=s, bs=16) for s in range(3)]
+        outs = [torch.empty_like(p.q) for p in probs]
+        graph = Graph(lambda: [paged_attention_append_meta(p.q, p.k, p.v, p.pool, 0, p.meta,
+                                                           out=o) for p, o in zip(probs, outs)])
+        n_per = len(probs)
     else:
-        p = workloads.cfg5_problem(dev, seed=0, bs=16)
-        out = torch.empty_like(p.q)
-        mk = int(p.lens.max())
-
-        def attn():
-            paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens,
-                             max_kv_len=mk, out=out)
-        nbytes = attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs)
+        probs = [workloads.cfg5_problem(dev, seed=s, bs=16) for s in range(5)]
+        outs = [torch.empty_like(p.q) for p in probs]
+        graph = Graph(lambda: [paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables,
+                                                p.seq_lens, max_kv_len=int(p.lens.max()), out=o)
+                               for p, o in zip(probs, outs)])
+        n_per = len(probs)
     for _ in range(args.profile_iters):
-        attn()
+        graph.replay()
     torch.cuda.synchronize()
     if args.copy_mib > 0:
         # an elementwise kernel (a same-dtype copy_ would be a DMA transfer,
@@ -385,8 +658,19 @@ def run_profile(args, torch):
         for _ in range(3):
             torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
-    log(f"profile {args.profile}: {args.profile_iters} attention launches of "
-        f"{nbytes} algorithmic bytes; copy {args.copy_mib} MiB x 3")
+    log(f"profile {args.profile}: {args.profile_iters} graph replays of {n_per} launches; "
+        f"copy {args.copy_mib} MiB x 3")
+
+
+def traffic_of(w):
+    """HBM bytes per launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by an elementwise kernel of known
+    size), or None."""
+    tpath = os.path.join(REPO, "profiles", f"traffic_{w}_attention.json")
+    if not os.path.exists(tpath):
+        return None
+    with open(tpath) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
 
 
 def main():
@@ -398,12 +682,15 @@ def main():
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
-    ap.add_argument("--profile", choices=["cfg4", "cfg5", "cfg5mixed", "model", "sampling"], default=None,
-                    help="run only the decode-attention launches of this workload "
-                         "(a rocprofv3 target); no JSON line")
+    ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--profile", choices=["cfg4", "cfg4step", "cfg5", "cfg5mixed", "model",
+                                          "sampling"], default=None,
+                    help="run only the launches of this workload (a rocprofv3 target); "
+                         "no JSON line")
     ap.add_argument("--profile-iters", type=int, default=20)
     ap.add_argument("--copy-mib", type=int, default=0,
-                    help="with --profile: also copy this many MiB device to device, 3 times")
+                    help="with --profile: also run an elementwise kernel over this many MiB, "
+                         "3 times")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -422,24 +709,20 @@ def main():
         run_profile(args, torch)
         return
 
-    hot = run_hot_path(args, torch)
+    st = build_cfg4_path(torch)
+    hot = run_hot_path(args, torch, st)
+    roof = run_roofline_cfg4(args, torch, st)
     value = hot["step_bytes"] / hot["step_sec"] / 1e9
     model = None if args.no_model else run_model(args, torch)
     ns = None if args.no_north_star else run_north_star(args, torch)
     mixed = None if args.no_north_star else run_mixed_step(args, torch)
-    cpu = None if args.no_cpu else run_cpu_baseline(hot, torch)
+    configs = None
+    if not args.no_configs:
+        configs = {"cfg1": run_cfg1(args, torch), "cfg2": run_cfg2(args, torch),
+                   "cfg3": run_cfg3(args, torch)}
+    cpu = None if args.no_cpu else run_cpu_baseline(st, model, torch)
 
-    achieved = hot["attn_bytes"] / hot["attn_sec"] / 1e9
-
-    def traffic_of(w):
-        # HBM bytes per attention op from the committed rocprofv3 counter
-        # summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size)
-        tpath = os.path.join(REPO, "profiles", f"traffic_{w}_attention.json")
-        if not os.path.exists(tpath):
-            return None
-        with open(tpath) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    traffic = traffic_of("cfg4")
+    achieved = roof["bytes"] / roof["cold_sec"] / 1e9
     if ns is not None:
         ns["traffic"] = traffic_of("cfg5")
     line = {
@@ -457,35 +740,40 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "cfg4 paged decode step: 12 layers x (slot-mapped KV append of 128 rows "
-                        "fused into the paged MQA decode attention), batch 128, Hq 16, Hkv 1, D 64, ctx "
-                        "U[256,2048] seed 0, block_size 16, 16384-block pool per layer",
+                        "fused into the paged MQA decode attention), batch 128, Hq 16, Hkv 1, D "
+                        "64, ctx U[256,2048] seed 0, block_size 16, 16384-block pool per layer; "
+                        "the 12 calls replayed from one HIP graph",
             "global_batch": 128,
             "layers": 12,
             "step_bytes": hot["step_bytes"],
             "parallelism": "none (1 GPU)",
         },
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "value_two_calls": round(hot["step_bytes"] / hot["step_sec_two_calls"] / 1e9, 2),
+        "value_eager_calls": round(hot["step_bytes"] / hot["eager_sec"] / 1e9, 2),
+        "value_two_calls_eager": round(hot["step_bytes"] / hot["two_calls_sec"] / 1e9, 2),
         "decode_tok_s": None if model is None else round(model["tok_s"], 1),
         "decode_step_ms": None if model is None else round(model["step_sec"] * 1e3, 4),
-        "decode_step": "the whole greedy decode step (12 layers + argmax + metadata advance) "
-                       "replayed from one HIP graph",
+        "decode_step": "the whole cfg4 greedy decode step (12 layers + argmax + metadata "
+                       "advance) replayed from one HIP graph",
         "decode_tok_s_eager": None if model is None else round(N_MODEL / model["eager_step_sec"], 1),
         "roofline": {
-            "kernel": "paged MQA decode attention, cfg4, one layer: decode_mfma_kernel "
-                      "(split-K partitions merged in-kernel by the last one to finish; one "
-                      "launch)",
+            "kernel": "paged MQA decode attention, cfg4, one layer: decode_mfma_kernel (split-K "
+                      "partitions merged in-kernel by the last one to finish); cold: a graph "
+                      "replay launches it on each of the 12 layers' pools in turn",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "bytes_per_launch": hot["attn_bytes"],
-            "us_per_launch": round(hot["attn_sec"] * 1e6, 3),
+            "traffic": traffic_of("cfg4"),
+            "bytes_per_launch": roof["bytes"],
+            "us_per_launch": round(roof["cold_sec"] * 1e6, 3),
+            "warm_us_per_launch": round(roof["warm_sec"] * 1e6, 3),
+            "warm_achieved": round(roof["bytes"] / roof["warm_sec"] / 1e9, 2),
         },
         "north_star": ns,
         "cfg5_mixed_step": mixed,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
