@@ -362,7 +362,9 @@ def run_model(args, torch):
     torch.cuda.synchronize()
     sec = time_events(graph.replay, steps, stream)
     log(f"model decode step, HIP graph: {sec * 1e3:.3f} ms, {N / sec:.0f} tok/s")
-    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    # fp32 CPU copy of the weights for the CPU baseline's model sample
+    sd = (None if args.no_cpu or args.profile else
+          {k: v.detach().float().cpu() for k, v in model.state_dict().items()})
     del graph, pool, model
     torch.cuda.empty_cache()
     return dict(step_sec=sec, tok_s=N / sec, eager_step_sec=eager, state_dict=sd, cfg=cfg,
@@ -569,7 +571,7 @@ def run_cpu_baseline(st, model, torch):
     res["cfg1_sample"] = "fp32 decode step of both sequences (positions 16-29), median of 10"
     log(f"cpu cfg1 model: {s1 * 1e3:.2f} ms/step, {2 / s1:.0f} tok/s")
     # cfg4 model sample on the CPU
-    if model is not None:
+    if model is not None and model["state_dict"] is not None:
         cfg = model["cfg"]
         ref4 = torch_ref.RefModel(model["state_dict"], cfg.num_layers, cfg.num_heads,
                                   cfg.num_kv_heads, cfg.max_seq_len)
