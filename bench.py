@@ -65,15 +65,17 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def attn_bytes(lens, hq, hkv, d, esize, bs):
+def attn_bytes(lens, hq, hkv, d, esize, bs, kv_esize=None):
     """Algorithmic bytes of one decode attention launch (the formula of the
     oracle's decode_attention_bytes, restated so the product bench does not
-    depend on the oracle): K+V rows of every visible token, Q in, O out,
-    4 B per block-table entry used, 4 B per seq_len."""
+    depend on the oracle): K+V rows of every visible token (kv_esize bytes
+    per element, 1 for fp8 pools), Q in, O out, 4 B per block-table entry
+    used, 4 B per seq_len."""
     kv = int(sum(int(x) for x in lens))
     n = len(lens)
     blocks = sum((int(x) + bs - 1) // bs for x in lens)
-    return kv * hkv * d * 2 * esize + 2 * n * hq * d * esize + 4 * blocks + 4 * n
+    kve = esize if kv_esize is None else kv_esize
+    return kv * hkv * d * 2 * kve + 2 * n * hq * d * esize + 4 * blocks + 4 * n
 
 
 def append_bytes(n_tok, hkv, d, esize, n_seq):
@@ -248,6 +250,20 @@ def run_north_star(args, torch):
     w_gbs = nb[0] / w / 1e9
     log(f"cfg5 attention: cold {c * 1e6:.2f} us ({c_gbs:.0f} GB/s, {100 * c_gbs / HBM_PEAK_GBS:.1f}%),"
         f" warm {w * 1e6:.2f} us ({w_gbs:.0f} GB/s)")
+    del cold, warm
+    # the same problems with fp8 pools (CacheConfig.kv_dtype = float8_e4m3fn):
+    # half the K/V bytes, Q and O still bf16
+    fp8 = torch.float8_e4m3fn
+    for p in probs:
+        p.k_pool = p.k_pool.to(fp8)
+        p.v_pool = p.v_pool.to(fp8)
+    torch.cuda.empty_cache()
+    cold8 = Graph(lambda: [launch(i) for i in range(len(probs))])
+    c8 = cold8.time(reps) / len(probs)
+    nb8 = [attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs, kv_esize=1) for p in probs]
+    g8 = sum(nb8) / len(nb8) / c8 / 1e9
+    log(f"cfg5 attention, fp8 pools: cold {c8 * 1e6:.2f} us ({g8:.0f} GB/s, "
+        f"{100 * g8 / HBM_PEAK_GBS:.1f}%), {sum(nb) / len(nb) / c8 / 1e9:.0f} GB/s bf16-equivalent")
     res = {"workload": "cfg5 paged MQA decode attention: batch 256, Hq 32, Hkv 1, D 128, bf16, "
                        "lognormal ctx mean 1024 cap 8192, bs 16, fragmented tables; cold = a "
                        "graph replaying one launch on each of 5 seeded problems (seeds 0-4, "
@@ -256,8 +272,14 @@ def run_north_star(args, torch):
            "us_per_launch": round(c * 1e6, 3), "bytes_per_launch": int(sum(nb) / len(nb)),
            "achieved_gbs": round(c_gbs, 1), "frac_of_peak": round(c_gbs / HBM_PEAK_GBS, 4),
            "warm_us_per_launch": round(w * 1e6, 3), "warm_bytes_per_launch": nb[0],
-           "warm_achieved_gbs": round(w_gbs, 1), "target_frac": 0.70}
-    del probs, outs, cold, warm
+           "warm_achieved_gbs": round(w_gbs, 1), "target_frac": 0.70,
+           "fp8_pools": {"us_per_launch": round(c8 * 1e6, 3),
+                         "bytes_per_launch": int(sum(nb8) / len(nb8)),
+                         "achieved_gbs": round(g8, 1), "frac_of_peak": round(g8 / HBM_PEAK_GBS, 4),
+                         "speedup_vs_bf16_pools": round(c / c8, 3),
+                         "note": "the same 5 problems with float8_e4m3fn K/V pools (Q and O "
+                                 "bf16); bytes counted at 1 B per K/V element"}}
+    del probs, outs, cold8
     torch.cuda.empty_cache()
     return res
 

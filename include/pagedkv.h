@@ -11,7 +11,12 @@
  *     Work is enqueued asynchronously; no entry point synchronises the host.
  *   - Return value: PKV_OK (0) or a negative PKV_ERR_* code; the message of
  *     the last failure on the calling thread is pkv_last_error().
- *   - `dtype` is one of PKV_DTYPE_*; K/V/Q/out share it.
+ *   - `dtype` is one of PKV_DTYPE_*; K/V/Q/out share it. OR-ing PKV_KV_FP8
+ *     into it declares fp8 pools: the pools hold fp8 e4m3 (OCP,
+ *     torch.float8_e4m3fn; 1 byte per element) while Q, out and the rows
+ *     appended keep the PKV_DTYPE_* type (KVPool with
+ *     CacheConfig.kv_dtype = torch.float8_e4m3fn, models/model_config.py:49,
+ *     :77-88).
  *   - Pool layout (per layer, per K or V): [num_blocks, block_size, hkv, d]
  *     contiguous, i.e. token slot `s` starts at element s * hkv * d.
  *   - `status` (nullable) is a device int32 word the kernels OR error bits
@@ -75,6 +80,12 @@ extern "C" {
 #define PKV_DTYPE_F32 0
 #define PKV_DTYPE_F16 1
 #define PKV_DTYPE_BF16 2
+/* Flag OR-ed into `dtype`: the K/V pools hold fp8 e4m3. Appends round each
+   new value to the nearest fp8 value (ties to even; magnitudes of 480 and
+   more, infinities and NaN give NaN), the bytes torch's conversion to
+   float8_e4m3fn gives; attention widens pool values exactly. Attention with
+   fp8 pools: bf16/f16 Q, 16 or 32 query heads per kv head, d = 64 or 128. */
+#define PKV_KV_FP8 0x100
 
 /* part_tokens values of pkv_paged_attention selecting the persistent decode
    kernel where it applies (bf16/f16, one query per sequence, 16 or 32
@@ -119,7 +130,8 @@ const char* pkv_last_error(void);
  * where a row is `row_elems` (= hkv * d) contiguous elements and
  * slot(t) = slot_mapping[t] (int64), wrapped by pool_slots when negative
  * (index_put semantics). Slots outside [-pool_slots, pool_slots) are skipped
- * and flagged PKV_STATUS_BAD_SLOT. Bit-exact copy.
+ * and flagged PKV_STATUS_BAD_SLOT. Bit-exact copy (with PKV_KV_FP8: each
+ * value rounded to fp8 as torch's index_put into a float8_e4m3fn pool does).
  * Replaces KVPool.write (serving/kv_pool.py:57-70).
  */
 int pkv_append(void* k_pool, void* v_pool, int64_t pool_slots,
@@ -148,7 +160,8 @@ int pkv_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
 /*
  * Gather one sequence's first seq_len token rows out of the pool into dense
  * k_out/v_out [seq_len, row_elems] following block_table (device int32,
- * n_blocks entries). Replaces KVPool.gather (serving/kv_pool.py:72-82).
+ * n_blocks entries), in the pool's element type (fp8 bytes with
+ * PKV_KV_FP8). Replaces KVPool.gather (serving/kv_pool.py:72-82).
  */
 int pkv_gather(void* k_out, void* v_out, const void* k_pool,
                const void* v_pool, int64_t num_blocks, int block_size,

@@ -182,6 +182,51 @@ def paged_attention(q, k_pool, v_pool, block_table, seq_lens, query_start_loc,
     return out, lse
 
 
+def e4m3_codes(x) -> np.ndarray:
+    """fp8 e4m3 bytes (OCP, torch.float8_e4m3fn) of float32 values, as the
+    reference's KVPool.write stores rows into a pool whose CacheConfig.kv_dtype
+    is float8_e4m3fn (models/model_config.py:49, serving/kv_pool.py:57-70:
+    index_put converts). Format: sign, 4 exponent bits (bias 7), 3 mantissa
+    bits; no infinities; S.1111.111 is NaN; largest finite 1.75 * 2^8 = 448;
+    below 2^-6 the values are the multiples of 2^-9. Rounding to nearest,
+    ties to even; a magnitude that rounds beyond 448 (>= 464), infinities
+    and NaN give NaN (0x7F with the sign)."""
+    x = np.asarray(x, dtype=np.float32)
+    sign = (np.signbit(x).astype(np.uint8) << 7)
+    with np.errstate(invalid="ignore"):  # signalling NaN inputs
+        a = np.abs(x.astype(np.float64))
+    out = np.zeros(x.shape, dtype=np.uint8)
+    nan = ~np.isfinite(a)
+    a = np.where(nan, 0.0, a)
+    sub = a < 2.0 ** -6
+    # subnormal range: m * 2^-9, m = round-half-even(a * 512) (m = 8 is 2^-6,
+    # whose code 0x08 is the first normal one)
+    m = np.rint(np.where(sub, a, 0.0) * 512.0)  # numpy rounds halves to even
+    out = np.where(sub, m.astype(np.int64), 0).astype(np.uint8)
+    # normal range: exponent e (2^e <= a < 2^(e+1)), 3-bit mantissa rounded
+    e = np.floor(np.log2(np.where(sub, 1.0, a)))
+    q = np.rint(np.where(sub, 1.0, a) / 2.0 ** e * 8.0)  # 8..16, halves to even
+    e = np.where(q >= 16, e + 1, e)
+    q = np.where(q >= 16, 8, q)
+    code = ((e + 7).astype(np.int64) << 3) | (q.astype(np.int64) - 8)
+    big = (~sub) & ((code > 0x7E) | (e + 7 > 15))
+    out = np.where(sub, out, np.clip(code, 0, 0x7F).astype(np.uint8))
+    out = np.where(big | nan, 0x7F, out).astype(np.uint8)
+    return out | sign
+
+
+def e4m3_values(codes) -> np.ndarray:
+    """float64 values of fp8 e4m3 bytes (the exact widening the attention
+    kernels read an fp8 pool with)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 15
+    m = c & 7
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    val = np.where((e == 15) & (m == 7), np.nan, val)
+    return sign * val
+
+
 def decode_attention_bytes(seq_lens, hq, hkv, d, elem_bytes, block_size):
     """Algorithmic HBM bytes of one paged decode attention call (one query per
     sequence): K and V rows of every visible token, Q and O, block-table

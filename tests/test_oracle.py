@@ -364,3 +364,29 @@ def test_rmsnorm_kat():
     y = torch_ref.rmsnorm(x, torch.tensor([1.0, 2.0]), eps=0.0)
     r = math.sqrt((9 + 16) / 2)
     assert torch.allclose(y, torch.tensor([[3 / r, 8 / r]]))
+
+
+def test_e4m3_codes_match_torch_and_the_format():
+    """The oracle's fp8 rounding (oracle.paged_ref.e4m3_codes) against torch's
+    conversion to float8_e4m3fn on every bf16 and fp16 value and a wide
+    random sample, and against the format's closed forms: the largest finite
+    value, the smallest subnormal, ties to even, NaN for overflow."""
+    import torch
+    for x in (torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float(),
+              torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16).float(),
+              torch.randn(1 << 18, generator=torch.Generator().manual_seed(0))
+              * torch.exp(4 * torch.randn(1 << 18, generator=torch.Generator().manual_seed(1)))):
+        want = x.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(ref.e4m3_codes(x.numpy()), want)
+    c = ref.e4m3_codes
+    assert c(448.0) == 0x7E and c(-448.0) == 0xFE          # largest finite
+    assert c(463.9) == 0x7E and c(464.0) == 0x7E          # tie below 480 goes to even (448)
+    assert c(464.01) == 0x7F and c(1e9) == 0x7F           # beyond: NaN, no infinity
+    assert c(np.inf) == 0x7F and c(-np.inf) == 0xFF and c(np.nan) == 0x7F
+    assert c(2.0 ** -9) == 0x01 and c(2.0 ** -10) == 0x00  # smallest subnormal; tie to even 0
+    assert c(3 * 2.0 ** -10) == 0x02                        # 1.5 ulp: tie to even (2)
+    assert c(1.0) == 0x38 and c(1.0625) == 0x38 and c(1.1875) == 0x3A
+    v = ref.e4m3_values(np.arange(256, dtype=np.uint8))
+    assert np.isnan(v[0x7F]) and np.isnan(v[0xFF]) and np.sum(np.isnan(v)) == 2
+    fin = ~np.isnan(v)
+    assert np.array_equal(ref.e4m3_codes(v[fin].astype(np.float32)), np.arange(256)[fin])

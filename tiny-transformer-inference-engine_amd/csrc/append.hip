@@ -147,6 +147,101 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
   }
 }
 
+// ---- fp8 pools: each thread converts one piece of 8 values (8 source
+// elements in, 8 bytes out) with f32_to_e4m3.
+template <typename S>
+__device__ __forceinline__ float elem_to_f32(S x) {
+  return (float)x;
+}
+template <>
+__device__ __forceinline__ float elem_to_f32<bf16>(bf16 x) {
+  return __uint_as_float((unsigned)__builtin_bit_cast(unsigned short, x) << 16);
+}
+
+template <typename S>
+__device__ __forceinline__ uint2 narrow_piece(const S* __restrict__ p) {
+  S v[8];
+  __builtin_memcpy(v, p, sizeof(v));  // one or two 16-byte loads (alignment checked on the host)
+  unsigned w[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e >> 2] |= f32_to_e4m3(elem_to_f32(v[e])) << (8 * (e & 3));
+  return uint2{w[0], w[1]};
+}
+
+template <typename S>
+__global__ __launch_bounds__(kThreads) void append_fp8_kernel(
+    char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t pool_slots,
+    const S* __restrict__ k_new, const S* __restrict__ v_new,
+    const int64_t* __restrict__ slots, int64_t n_tok, int64_t row_elems, int* status) {
+  const int64_t ppr = row_elems / 8;
+  const int64_t total = n_tok * ppr;
+  const S* __restrict__ src = blockIdx.y ? v_new : k_new;
+  char* __restrict__ dst = blockIdx.y ? v_pool : k_pool;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += stride) {
+    const int64_t tok = i / ppr;
+    const int64_t pc = i - tok * ppr;
+    int64_t slot = slots[tok];
+    if (!resolve_slot(slot, pool_slots)) {
+      if (status && pc == 0 && blockIdx.y == 0) atomicOr(status, PKV_STATUS_BAD_SLOT);
+      continue;
+    }
+    *reinterpret_cast<uint2*>(dst + slot * row_elems + pc * 8) =
+        narrow_piece(src + tok * row_elems + pc * 8);
+  }
+}
+
+template <typename S>
+__global__ __launch_bounds__(kThreads) void append_table_fp8_kernel(
+    char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t num_blocks, int bs_shift,
+    const S* __restrict__ k_new, const S* __restrict__ v_new,
+    const int32_t* __restrict__ tables, int max_blk, const int32_t* __restrict__ qloc,
+    const int32_t* __restrict__ start_pos, int n_seq, int64_t n_tok, int64_t row_elems,
+    int min_qlen, int* status) {
+  const int64_t ppr = row_elems / 8;
+  const int64_t total = n_tok * ppr;
+  const S* __restrict__ src = blockIdx.y ? v_new : k_new;
+  char* __restrict__ dst = blockIdx.y ? v_pool : k_pool;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += stride) {
+    const int64_t tok = i / ppr;
+    const int64_t pc = i - tok * ppr;
+    const int s = seq_of_token(qloc, n_seq, tok);
+    if (min_qlen > 1 && qloc[s + 1] - qloc[s] < min_qlen) continue;
+    const int64_t pos = (int64_t)start_pos[s] + (tok - qloc[s]);
+    const int64_t page = pos >> bs_shift;
+    const bool flag = status && pc == 0 && blockIdx.y == 0;
+    if (pos < 0 || page >= max_blk) {
+      if (flag) atomicOr(status, PKV_STATUS_SHORT_TABLE);
+      continue;
+    }
+    const int64_t phys = tables[(int64_t)s * max_blk + page];
+    if (phys <= 0 || phys >= num_blocks) {
+      if (flag) atomicOr(status, PKV_STATUS_BAD_BLOCK);
+      continue;
+    }
+    const int64_t slot = (phys << bs_shift) + (pos & ((1 << bs_shift) - 1));
+    *reinterpret_cast<uint2*>(dst + slot * row_elems + pc * 8) =
+        narrow_piece(src + tok * row_elems + pc * 8);
+  }
+}
+
+// 8-byte pool pieces and 8-element source pieces must be naturally aligned.
+int check_fp8_rows(int64_t row_elems, int src_dtype, std::initializer_list<const void*> pools,
+                   std::initializer_list<const void*> srcs) {
+  if (row_elems % 8 != 0)
+    return fail(PKV_ERR_UNSUPPORTED, "fp8 append: row of %lld elements (need a multiple of 8)",
+                (long long)row_elems);
+  const uintptr_t sa = (uintptr_t)8 * elem_bytes(src_dtype);
+  for (const void* p : pools)
+    if ((uintptr_t)p % 8) return fail(PKV_ERR_UNSUPPORTED, "fp8 append: pool not 8-byte aligned");
+  for (const void* p : srcs)
+    if ((uintptr_t)p % (sa < 16 ? sa : 16))
+      return fail(PKV_ERR_UNSUPPORTED, "fp8 append: source rows not %zu-byte aligned",
+                  (size_t)(sa < 16 ? sa : 16));
+  return PKV_OK;
+}
+
 // Widest piece (16/8/4/2 bytes) dividing the row and every base pointer.
 int pick_vec(int64_t row_bytes, std::initializer_list<const void*> ptrs) {
   uintptr_t acc = (uintptr_t)row_bytes;
@@ -214,6 +309,46 @@ int launch_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
   }
 #undef PKV_APPEND_T
   return check_launch("append_table_kernel");
+}
+
+int launch_append_fp8(void* k_pool, void* v_pool, int64_t pool_slots, const void* k_new,
+                      const void* v_new, const int64_t* slots, int64_t n_tok,
+                      int64_t row_elems, int src_dtype, int* status, hipStream_t stream) {
+  if (n_tok == 0) return PKV_OK;
+  int rc = check_fp8_rows(row_elems, src_dtype, {k_pool, v_pool}, {k_new, v_new});
+  if (rc != PKV_OK) return rc;
+  const dim3 grid = copy_grid(n_tok * (row_elems / 8));
+#define PKV_APPEND8(S)                                                                       \
+  hipLaunchKernelGGL(append_fp8_kernel<S>, grid, dim3(kThreads), 0, stream, (char*)k_pool,   \
+                     (char*)v_pool, pool_slots, (const S*)k_new, (const S*)v_new, slots,     \
+                     n_tok, row_elems, status)
+  if (src_dtype == PKV_DTYPE_BF16) PKV_APPEND8(bf16);
+  else if (src_dtype == PKV_DTYPE_F16) PKV_APPEND8(f16);
+  else PKV_APPEND8(float);
+#undef PKV_APPEND8
+  return check_launch("append_fp8_kernel");
+}
+
+int launch_append_from_table_fp8(void* k_pool, void* v_pool, int64_t num_blocks, int bs_shift,
+                                 const void* k_new, const void* v_new,
+                                 const int32_t* block_tables, int max_blk, const int32_t* qloc,
+                                 const int32_t* start_pos, int n_seq, int64_t n_tok,
+                                 int64_t row_elems, int src_dtype, int min_qlen, int* status,
+                                 hipStream_t stream) {
+  if (n_tok == 0 || n_seq == 0) return PKV_OK;
+  int rc = check_fp8_rows(row_elems, src_dtype, {k_pool, v_pool}, {k_new, v_new});
+  if (rc != PKV_OK) return rc;
+  const dim3 grid = copy_grid(n_tok * (row_elems / 8));
+#define PKV_APPEND8_T(S)                                                                    \
+  hipLaunchKernelGGL(append_table_fp8_kernel<S>, grid, dim3(kThreads), 0, stream,           \
+                     (char*)k_pool, (char*)v_pool, num_blocks, bs_shift, (const S*)k_new,   \
+                     (const S*)v_new, block_tables, max_blk, qloc, start_pos, n_seq, n_tok, \
+                     row_elems, min_qlen, status)
+  if (src_dtype == PKV_DTYPE_BF16) PKV_APPEND8_T(bf16);
+  else if (src_dtype == PKV_DTYPE_F16) PKV_APPEND8_T(f16);
+  else PKV_APPEND8_T(float);
+#undef PKV_APPEND8_T
+  return check_launch("append_table_fp8_kernel");
 }
 
 int launch_gather(void* k_out, void* v_out, const void* k_pool,

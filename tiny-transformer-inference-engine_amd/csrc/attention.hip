@@ -327,6 +327,9 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,
                         int part_tokens, int dtype) {
   AttnPlan p{};
+  // fp8 pools are read by the MFMA kernels only (rows widened in LDS)
+  const bool kv8 = dtype_kv8(dtype);
+  dtype = dtype_base(dtype);
   const int group = hq / hkv;
   // the MFMA kernels read table entry 0 of a row unconditionally: with no
   // table (every context empty) the generic kernel writes the empty rows
@@ -363,6 +366,10 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
     p.part_tokens = 0;
     p.parts_max = 1;
     p.ws_bytes = 0;
+    return p;
+  }
+  if (kv8 && !mfma) {
+    p.kind = -1;  // unsupported: reported by launch_attention
     return p;
   }
   p.kind = mfma ? 1 : 0;
@@ -405,7 +412,7 @@ AttnSplit plan_split(int n_seq, int max_q_len, int hq, int hkv, int d, int max_b
                      bool has_qloc) {
   AttnSplit sp{};
   sp.mixed = has_qloc && max_q_len > 1 && n_seq >= 2 && max_blk >= 1 &&
-             decode_mfma_supported(dtype, 1, hq / hkv, d);
+             decode_mfma_supported(dtype_base(dtype), 1, hq / hkv, d);
   if (!sp.mixed) {
     sp.dec = plan_attention(n_seq, max_q_len, hq, hkv, d, max_blk, block_size, max_kv_len,
                             part_tokens, dtype);
@@ -437,6 +444,10 @@ int device_cu_count() {
 int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
                      hipStream_t stream) {
   if (a.n_seq == 0) return PKV_OK;
+  if (p.kind < 0)
+    return fail(PKV_ERR_UNSUPPORTED,
+                "fp8 KV pools need bf16/f16 queries, 16 or 32 query heads per kv head and "
+                "head dim 64 or 128 (got group %d, d %d)", a.group, a.d);
   if (p.parts_max > 65535 || p.tiles_max > 65535)
     return fail(PKV_ERR_UNSUPPORTED, "attention grid too large (%d parts, %d tiles, %d seq*hkv)",
                 p.parts_max, p.tiles_max, a.n_seq * a.hkv);

@@ -38,6 +38,9 @@ static bool valid_dtype(int dtype) {
          dtype == PKV_DTYPE_BF16;
 }
 
+// A dtype argument: one PKV_DTYPE_* value, optionally with PKV_KV_FP8.
+static bool valid_dtype_arg(int dtype) { return valid_dtype(dtype_base(dtype)); }
+
 static int log2_exact(int64_t v) {
   if (v <= 0 || (v & (v - 1)) != 0) return -1;
   int s = 0;
@@ -60,13 +63,16 @@ int pkv_append(void* k_pool, void* v_pool, int64_t pool_slots,
                const int64_t* slot_mapping, int64_t n_tok, int64_t row_elems,
                int dtype, int* status, void* stream) {
   g_err[0] = 0;
-  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!valid_dtype_arg(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
   if (n_tok < 0 || row_elems <= 0 || pool_slots < 0)
     return fail(PKV_ERR_INVALID, "bad sizes n_tok=%lld row_elems=%lld pool_slots=%lld",
                 (long long)n_tok, (long long)row_elems, (long long)pool_slots);
   if (n_tok == 0) return PKV_OK;
   if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping)
     return fail(PKV_ERR_INVALID, "null pointer argument");
+  if (dtype_kv8(dtype))
+    return launch_append_fp8(k_pool, v_pool, pool_slots, k_new, v_new, slot_mapping, n_tok,
+                             row_elems, dtype_base(dtype), status, (hipStream_t)stream);
   return launch_append(k_pool, v_pool, pool_slots, k_new, v_new, slot_mapping,
                        n_tok, row_elems * elem_bytes(dtype), status,
                        (hipStream_t)stream);
@@ -80,7 +86,7 @@ int pkv_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
                           int64_t row_elems, int dtype, int* status,
                           void* stream) {
   g_err[0] = 0;
-  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!valid_dtype_arg(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
   const int bs_shift = log2_exact(block_size);
   if (bs_shift < 0)
     return fail(PKV_ERR_INVALID, "blocksize %d must be a power of two", block_size);
@@ -90,6 +96,11 @@ int pkv_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
   if (!k_pool || !v_pool || !k_new || !v_new || !block_tables ||
       !query_start_loc || !start_pos)
     return fail(PKV_ERR_INVALID, "null pointer argument");
+  if (dtype_kv8(dtype))
+    return launch_append_from_table_fp8(
+        k_pool, v_pool, num_blocks, bs_shift, k_new, v_new, block_tables, max_blk,
+        query_start_loc, start_pos, n_seq, n_tok, row_elems, dtype_base(dtype), 0, status,
+        (hipStream_t)stream);
   return launch_append_from_table(
       k_pool, v_pool, num_blocks, bs_shift, k_new, v_new, block_tables,
       max_blk, query_start_loc, start_pos, n_seq, n_tok,
@@ -101,7 +112,7 @@ int pkv_gather(void* k_out, void* v_out, const void* k_pool,
                const int32_t* block_table, int n_blocks, int seq_len,
                int64_t row_elems, int dtype, int* status, void* stream) {
   g_err[0] = 0;
-  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!valid_dtype_arg(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
   const int bs_shift = log2_exact(block_size);
   if (bs_shift < 0)
     return fail(PKV_ERR_INVALID, "blocksize %d must be a power of two", block_size);
@@ -116,7 +127,7 @@ int pkv_gather(void* k_out, void* v_out, const void* k_pool,
     return fail(PKV_ERR_INVALID, "null pointer argument");
   return launch_gather(k_out, v_out, k_pool, v_pool, num_blocks, bs_shift,
                        block_table, n_blocks, seq_len,
-                       row_elems * elem_bytes(dtype), status,
+                       row_elems * (dtype_kv8(dtype) ? 1 : elem_bytes(dtype_base(dtype))), status,
                        (hipStream_t)stream);
 }
 
@@ -148,7 +159,11 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
                    int* status, void* stream, const void* k_new, const void* v_new,
                    const int32_t* start_pos) {
   g_err[0] = 0;
-  if (!valid_dtype(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!valid_dtype_arg(dtype)) return fail(PKV_ERR_INVALID, "unknown dtype %d", dtype);
+  const bool kv8 = dtype_kv8(dtype);
+  const int qdtype = dtype_base(dtype);  // Q, out, k_new / v_new
+  if (kv8 && qdtype == PKV_DTYPE_F32)
+    return fail(PKV_ERR_UNSUPPORTED, "fp8 KV pools need bf16 or f16 queries");
   if (hkv <= 0 || hq <= 0 || hq % hkv != 0)
     return fail(PKV_ERR_INVALID, "Hq (%d) must be a multiple of Hkv (%d)", hq, hkv);
   if (d <= 0 || d % 8 != 0)
@@ -196,6 +211,7 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
   base.d = d;
   base.scale_log2 = sc * 1.4426950408889634f;
   base.causal = causal ? 1 : 0;
+  base.kv8 = kv8 ? 1 : 0;
   base.status = status;
   // one launch's view: its plan's geometry and workspace layout (partials
   // live after the record region, see kWsCounterBytes)
@@ -214,7 +230,19 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     a.ws_ml = ws ? ws + units * plan.rows * (size_t)d : nullptr;
     return a;
   };
-  const int64_t row_bytes = (int64_t)hkv * d * elem_bytes(dtype);
+  const int64_t row_bytes = (int64_t)hkv * d * elem_bytes(qdtype);
+  // the table append of rows the decode kernel does not take fused
+  auto append_rows = [&](int min_qlen) {
+    if (kv8)
+      return launch_append_from_table_fp8(
+          const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
+          v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens,
+          (int64_t)hkv * d, qdtype, min_qlen, status, (hipStream_t)stream);
+    return launch_append_from_table(
+        const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
+        v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens, row_bytes,
+        min_qlen, status, (hipStream_t)stream);
+  };
   // Only the split-K partition decode kernel takes the append fused: for
   // the persistent kernel the fused form measured slower than a separate
   // append launch (register pressure at 32 heads x 128 dims), and the
@@ -224,10 +252,7 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     if (k_new) {
       if (sp.dec.kind != 1) {
         // append, then attend
-        const int rc = launch_append_from_table(
-            const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
-            v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens,
-            row_bytes, 0, status, (hipStream_t)stream);
+        const int rc = append_rows(0);
         if (rc != PKV_OK) return rc;
       } else {
         a.k_new = k_new;
@@ -235,7 +260,7 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
         a.new_pos = start_pos;
       }
     }
-    return launch_attention(a, sp.dec, dtype, (hipStream_t)stream);
+    return launch_attention(a, sp.dec, qdtype, (hipStream_t)stream);
   }
   // mixed batch: the decode sequences on an MFMA decode kernel, then the
   // prefill sequences; the prefill rows (and the decode rows unless the
@@ -244,10 +269,7 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
   const AttnArgs ap = args_for(sp.pre, 2);
   if (k_new) {
     const bool fuse = sp.dec.kind == 1;
-    const int rc = launch_append_from_table(
-        const_cast<void*>(k_pool), const_cast<void*>(v_pool), num_blocks, bs_shift, k_new,
-        v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens, row_bytes,
-        fuse ? 2 : 0, status, (hipStream_t)stream);
+    const int rc = append_rows(fuse ? 2 : 0);
     if (rc != PKV_OK) return rc;
     if (fuse) {
       ad.k_new = k_new;
@@ -255,9 +277,9 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
       ad.new_pos = start_pos;
     }
   }
-  int rc = launch_attention(ad, sp.dec, dtype, (hipStream_t)stream);
+  int rc = launch_attention(ad, sp.dec, qdtype, (hipStream_t)stream);
   if (rc != PKV_OK) return rc;
-  return launch_attention(ap, sp.pre, dtype, (hipStream_t)stream);
+  return launch_attention(ap, sp.pre, qdtype, (hipStream_t)stream);
 }
 
 // Scratch of pkv_paged_attention_noalloc: one array per device, in the

@@ -31,8 +31,9 @@ static_assert(kBlock >= kTblCap, "one thread per table entry of a window");
 
 // PF = chunks each wavefront keeps in flight in registers; OCC = wavefronts
 // per SIMD the register budget is sized for; APP = the fused append of
-// a.k_new / a.v_new at a.new_pos (compiled out of the plain attention).
-template <typename T, int D, int NT, int PF, int OCC, bool OFF64, bool APP>
+// a.k_new / a.v_new at a.new_pos (compiled out of the plain attention); KV8 =
+// fp8 pools (rows widened to T when staged in LDS).
+template <typename T, int D, int NT, int PF, int OCC, bool OFF64, bool APP, bool KV8>
 __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -78,8 +79,8 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   PoolView pv;
   pv.kbase = static_cast<const char*>(a.k_pool);
   pv.vbase = static_cast<const char*>(a.v_pool);
-  pv.row_stride = (int64_t)a.hkv * D * 2;
-  pv.head_off = (int64_t)kvh * D * 2;
+  pv.row_stride = (int64_t)a.hkv * D * (KV8 ? 1 : 2);
+  pv.head_off = (int64_t)kvh * D * (KV8 ? 1 : 2);
   pv.num_blocks = (int)a.num_blocks;
   pv.bs_shift = a.bs_shift;
   ChunkCtx cx;
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
       for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
     }
     __syncthreads();
-    run_chunks<T, D, NT, PF, OFF64, APP>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+    run_chunks<T, D, NT, PF, OFF64, APP, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
     last_blk_lo = cx.blk_lo;
     last_nblk = nblk;
   }
@@ -147,7 +148,8 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, g.q_begin, kvh, threadIdx.x),
                                     threadIdx.x);
     // each thread stores the piece it put into the buffer itself
-    store_new_row<D>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk, threadIdx.x);
+    store_new_row<T, D, KV8>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk,
+                             threadIdx.x);
   }
 
   // ---- merge the 4 wavefronts' partial states through LDS ----
@@ -288,15 +290,22 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
-// <T, D, NT, PF, OCC, OFF64, APP>: two wavefronts per SIMD
+// <T, D, NT, PF, OCC, OFF64, APP, KV8>: two wavefronts per SIMD
+template <typename T, int D, int NT, int PF, bool OFF64, bool KV8>
+void launch_k(const AttnArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.new_pos)
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, true, KV8>), grid,
+                       dim3(kBlock), 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, false, KV8>), grid,
+                       dim3(kBlock), 0, stream, a);
+}
 template <typename T, int D, int NT, int PF, bool OFF64>
 void launch_v(const AttnArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.new_pos)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, true>), grid, dim3(kBlock), 0,
-                       stream, a);
+  if (a.kv8)
+    launch_k<T, D, NT, PF, OFF64, true>(a, grid, stream);
   else
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, false>), grid, dim3(kBlock),
-                       0, stream, a);
+    launch_k<T, D, NT, PF, OFF64, false>(a, grid, stream);
 }
 
 template <typename T, bool OFF64>
@@ -326,7 +335,8 @@ bool decode_mfma_supported(int dtype, int max_q_len, int group, int d) {
 }
 
 bool pool_needs_off64(const AttnArgs& a) {
-  const int64_t pool_bytes = (a.num_blocks * ((int64_t)a.hkv * a.d * 2)) << a.bs_shift;
+  const int64_t pool_bytes = (a.num_blocks * ((int64_t)a.hkv * a.d * (a.kv8 ? 1 : 2)))
+                            << a.bs_shift;
   return pool_bytes >= (int64_t(1) << 31);
 }
 

@@ -193,7 +193,7 @@ __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, in
   if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
-template <typename T, int D, int NT, int PF, bool OFF64>
+template <typename T, int D, int NT, int PF, bool OFF64, bool KV8>
 __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs k) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   PoolView pv;
   pv.kbase = static_cast<const char*>(a.k_pool);
   pv.vbase = static_cast<const char*>(a.v_pool);
-  pv.row_stride = (int64_t)a.hkv * D * 2;
+  pv.row_stride = (int64_t)a.hkv * D * (KV8 ? 1 : 2);
   pv.num_blocks = (int)a.num_blocks;
   pv.bs_shift = a.bs_shift;
   ChunkCtx cx;
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     NewRow nr;  // no appended row: the library appends before this kernel
     nr.pos = -1;
     nr.lds = nullptr;
-    pv.head_off = (int64_t)kvh * D * 2;
+    pv.head_off = (int64_t)kvh * D * (KV8 ? 1 : 2);
     const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
     WaveState<NT, DT> st;
     st.reset();
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
         for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
       }
       __syncthreads();
-      run_chunks<T, D, NT, PF, OFF64, false>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+      run_chunks<T, D, NT, PF, OFF64, false, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
     }
 
     // ---- the next segment: its Q and first table window are loaded now
@@ -478,8 +478,12 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
 template <typename T, int D, int NT, int PF, bool OFF64>
 int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
   k.n_wg = sk_workgroups(D, 16 * NT);
-  hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64>), dim3(k.n_wg), dim3(kBlock), 0,
-                     stream, a, k);
+  if (a.kv8)
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, true>), dim3(k.n_wg), dim3(kBlock),
+                       0, stream, a, k);
+  else
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, false>), dim3(k.n_wg),
+                       dim3(kBlock), 0, stream, a, k);
   return check_launch("decode_sk_kernel");
 }
 

@@ -30,6 +30,7 @@ namespace mfma {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
@@ -48,6 +49,67 @@ struct Ops<f16> {
   static __device__ __forceinline__ floatx4 mma(v8 a, v8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
+};
+
+// fp8 pools: widening to bf16 / fp16 is exact; gfx950's
+// v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1 turns two fp8 bytes into two
+// 16-bit values. Narrowing (new rows) is f32_to_e4m3.
+template <typename T>
+struct Fp8;
+template <>
+struct Fp8<bf16> {
+  // bytes 0-1 / 2-3 of w as two bf16 (low half = the lower byte)
+  static __device__ __forceinline__ unsigned lo2(unsigned w) {
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+  }
+  static __device__ __forceinline__ unsigned hi2(unsigned w) {
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+  }
+  static __device__ __forceinline__ float to_f32(unsigned short h) {
+    return __uint_as_float((unsigned)h << 16);
+  }
+};
+template <>
+struct Fp8<f16> {
+  static __device__ __forceinline__ unsigned lo2(unsigned w) {
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+  }
+  static __device__ __forceinline__ unsigned hi2(unsigned w) {
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+  }
+  static __device__ __forceinline__ float to_f32(unsigned short h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
+};
+
+// 8 fp8 values (8 bytes) -> 8 values of T (16 bytes), element order kept
+template <typename T>
+__device__ __forceinline__ u32x4 widen8(u32x2 p) {
+  return u32x4{Fp8<T>::lo2(p.x), Fp8<T>::hi2(p.x), Fp8<T>::lo2(p.y), Fp8<T>::hi2(p.y)};
+}
+// 8 values of T -> 8 fp8 values, rounded as f32_to_e4m3
+template <typename T>
+__device__ __forceinline__ u32x2 narrow8(u32x4 p) {
+  unsigned out[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const unsigned short h = (unsigned short)(p[e >> 1] >> (16 * (e & 1)));
+    out[e >> 2] |= f32_to_e4m3(Fp8<T>::to_f32(h)) << (8 * (e & 3));
+  }
+  return u32x2{out[0], out[1]};
+}
+
+// One 16-byte piece (8 elements) of a K or V row as loaded from the pool:
+// 16 bytes from a 16-bit pool, 8 from an fp8 pool.
+template <bool KV8>
+struct PoolPiece {
+  typedef u32x4 type;
+  static constexpr int kBytes = 16;
+};
+template <>
+struct PoolPiece<true> {
+  typedef u32x2 type;
+  static constexpr int kBytes = 8;
 };
 
 constexpr int kTblCap = 256;  // block-table entries staged in LDS at a time
@@ -73,11 +135,12 @@ struct ChunkGeo {
 };
 
 // K and V rows of one 32-token chunk held in registers between their loads
-// and their LDS stores; bit j of `valid` clears row load j (bad table entry).
-template <int NPL>
+// and their LDS stores (as loaded: fp8 bytes from an fp8 pool); bit j of
+// `valid` clears row load j (bad table entry).
+template <int NPL, bool KV8>
 struct ChunkRegs {
-  u32x4 k[NPL];
-  u32x4 v[NPL];
+  typename PoolPiece<KV8>::type k[NPL];
+  typename PoolPiece<KV8>::type v[NPL];
   unsigned valid;
 };
 
@@ -85,7 +148,7 @@ struct ChunkRegs {
 struct PoolView {
   const char* kbase;
   const char* vbase;
-  int64_t row_stride;  // bytes per pool slot (hkv * d * 2)
+  int64_t row_stride;  // bytes per pool slot (hkv * d * element bytes)
   int64_t head_off;    // byte offset of this kv head inside a slot
   int num_blocks;
   int bs_shift;
@@ -114,9 +177,11 @@ struct ChunkCtx {
 // result, so the loads stay in flight until the chunk is staged.
 // OFF64 = false when every byte offset of the pool fits in 31 bits: the load
 // is then a uniform base plus a 32-bit per-lane offset.
-template <class Geo, int NPL, bool OFF64>
-__device__ __forceinline__ void load_chunk(ChunkRegs<NPL>& r, const PoolView& pv,
+template <class Geo, int NPL, bool OFF64, bool KV8>
+__device__ __forceinline__ void load_chunk(ChunkRegs<NPL, KV8>& r, const PoolView& pv,
                                            const ChunkCtx& cx, int c) {
+  typedef typename PoolPiece<KV8>::type P;
+  constexpr int PB = PoolPiece<KV8>::kBytes;
   const int bs_mask = (1 << pv.bs_shift) - 1;
   const int cb = cx.seg_lo + c * kChunk;
   unsigned vmask = 0;
@@ -130,14 +195,14 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NPL>& r, const PoolView& pv
     vmask |= (unsigned)ok << j;
     const int slot = ((ok ? phys : 0) << pv.bs_shift) + (pos & bs_mask);
     if constexpr (OFF64) {
-      const int64_t off = (int64_t)slot * pv.row_stride + pv.head_off + cx.pcol * 16;
-      r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.kbase + off));
-      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.vbase + off));
+      const int64_t off = (int64_t)slot * pv.row_stride + pv.head_off + cx.pcol * PB;
+      r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.kbase + off));
+      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.vbase + off));
     } else {
       const unsigned off = (unsigned)slot * (unsigned)pv.row_stride +
-                           (unsigned)pv.head_off + (unsigned)(cx.pcol * 16);
-      r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.kbase + off));
-      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv.vbase + off));
+                           (unsigned)pv.head_off + (unsigned)(cx.pcol * PB);
+      r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.kbase + off));
+      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.vbase + off));
     }
   }
   r.valid = vmask;
@@ -193,14 +258,17 @@ struct NewRow {
 };
 
 // Overwrites the staged row of token nr.pos when it lies in the chunk that
-// starts at token cb (its pool row may not be written yet).
-template <class Geo>
+// starts at token cb (its pool row may not be written yet). With an fp8 pool
+// the row is rounded to fp8 and widened back: attention sees the values the
+// pool will hold.
+template <typename T, class Geo, bool KV8>
 __device__ __forceinline__ void stage_new_row(const NewRow& nr, int cb, const ChunkCtx& cx,
                                               int lane) {
   if (nr.pos >= cb && nr.pos < cb + kChunk) {  // uniform across the wavefront
     const int r = nr.pos - cb;
     if (lane < 2 * Geo::CPR) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(nr.lds + lane * 16);
+      u32x4 x = *reinterpret_cast<const u32x4*>(nr.lds + lane * 16);
+      if constexpr (KV8) x = widen8<T>(narrow8<T>(x));
       char* dst = lane < Geo::CPR ? cx.kl + Geo::off(r, lane)
                                   : cx.vl + Geo::off(r, lane - Geo::CPR);
       *reinterpret_cast<u32x4*>(dst) = x;
@@ -208,10 +276,10 @@ __device__ __forceinline__ void stage_new_row(const NewRow& nr, int cb, const Ch
   }
 }
 
-// Registers -> this wavefront's LDS slice (rows with a bad table entry are
-// zeroed and flagged).
-template <class Geo, int NPL>
-__device__ __forceinline__ void stage_chunk(const ChunkRegs<NPL>& r, const ChunkCtx& cx,
+// Registers -> this wavefront's LDS slice, widened to T from an fp8 pool
+// (rows with a bad table entry are zeroed and flagged).
+template <typename T, class Geo, int NPL, bool KV8>
+__device__ __forceinline__ void stage_chunk(const ChunkRegs<NPL, KV8>& r, const ChunkCtx& cx,
                                             bool& bad_block) {
   asm volatile("" ::: "memory");
   const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
@@ -220,8 +288,16 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<NPL>& r, const Chunk
     const int row = cx.prow + j * Geo::ROWS_PER_LOAD;
     const bool ok = (r.valid >> j) & 1;
     bad_block |= !ok;
-    *reinterpret_cast<u32x4*>(cx.kl + Geo::off(row, cx.pcol)) = ok ? r.k[j] : zero;
-    *reinterpret_cast<u32x4*>(cx.vl + Geo::off(row, cx.pcol)) = ok ? r.v[j] : zero;
+    u32x4 kp, vp;
+    if constexpr (KV8) {
+      kp = widen8<T>(r.k[j]);
+      vp = widen8<T>(r.v[j]);
+    } else {
+      kp = r.k[j];
+      vp = r.v[j];
+    }
+    *reinterpret_cast<u32x4*>(cx.kl + Geo::off(row, cx.pcol)) = ok ? kp : zero;
+    *reinterpret_cast<u32x4*>(cx.vl + Geo::off(row, cx.pcol)) = ok ? vp : zero;
   }
 }
 
@@ -352,15 +428,16 @@ __device__ __forceinline__ void compute_chunk(int c, const ChunkCtx& cx,
 // One chunk: registers -> LDS slice, optionally refill the registers with
 // chunk `c + ahead` (issued before any compute so the loads overlap it),
 // then QK / softmax / PV out of LDS.
-template <typename T, int D, int NT, int NPL, bool OFF64, bool APP>
+template <typename T, int D, int NT, int NPL, bool OFF64, bool APP, bool KV8>
 __device__ __forceinline__ void chunk_step(
-    ChunkRegs<NPL>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
+    ChunkRegs<NPL, KV8>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
     const PoolView& pv, const typename Ops<T>::v8 (&qf)[NT][D / 32],
     WaveState<NT, D / 16>& st, bool& bad_block, const NewRow& nr) {
   using Geo = ChunkGeo<D>;
-  stage_chunk<Geo, NPL>(r, cx, bad_block);
-  if constexpr (APP) stage_new_row<Geo>(nr, cx.seg_lo + c * kChunk, cx, (int)(threadIdx.x & 63));
-  if (refill) load_chunk<Geo, NPL, OFF64>(r, pv, cx, c + ahead);
+  stage_chunk<T, Geo, NPL, KV8>(r, cx, bad_block);
+  if constexpr (APP)
+    stage_new_row<T, Geo, KV8>(nr, cx.seg_lo + c * kChunk, cx, (int)(threadIdx.x & 63));
+  if (refill) load_chunk<Geo, NPL, OFF64, KV8>(r, pv, cx, c + ahead);
   compute_chunk<T, D, NT>(c, cx, qf, st);
 }
 
@@ -369,7 +446,7 @@ __device__ __forceinline__ void chunk_step(
 // appended row nr is staged over its pool row where it falls). A
 // steady-state loop with no data-dependent branch keeps the compiler's wait
 // counts exact (staging buffer b waits only for buffer b's loads).
-template <typename T, int D, int NT, int PF, bool OFF64, bool APP>
+template <typename T, int D, int NT, int PF, bool OFF64, bool APP, bool KV8>
 __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
                                            const PoolView& pv,
                                            const typename Ops<T>::v8 (&qf)[NT][D / 32],
@@ -379,28 +456,28 @@ __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
   constexpr int NPL = Geo::NPL;
   const int nchunks = (cx.seg_hi - cx.seg_lo + kChunk - 1) / kChunk;
   const int step = nw * PF;
-  ChunkRegs<NPL> rb[PF];
+  ChunkRegs<NPL, KV8> rb[PF];
 #pragma unroll
   for (int b = 0; b < PF; ++b)
-    if (w + nw * b < nchunks) load_chunk<Geo, NPL, OFF64>(rb[b], pv, cx, w + nw * b);
+    if (w + nw * b < nchunks) load_chunk<Geo, NPL, OFF64, KV8>(rb[b], pv, cx, w + nw * b);
   int c = w;
   for (; c + nw * (2 * PF - 1) < nchunks; c += step) {
 #pragma unroll
     for (int b = 0; b < PF; ++b)
-      chunk_step<T, D, NT, NPL, OFF64, APP>(rb[b], c + nw * b, true, step, cx, pv, qf, st,
-                                       bad_block, nr);
+      chunk_step<T, D, NT, NPL, OFF64, APP, KV8>(rb[b], c + nw * b, true, step, cx, pv, qf, st,
+                                                 bad_block, nr);
   }
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
-      chunk_step<T, D, NT, NPL, OFF64, APP>(rb[b], c + nw * b, c + nw * (b + PF) < nchunks, step,
-                                       cx, pv, qf, st, bad_block, nr);
+      chunk_step<T, D, NT, NPL, OFF64, APP, KV8>(rb[b], c + nw * b, c + nw * (b + PF) < nchunks,
+                                                 step, cx, pv, qf, st, bad_block, nr);
   c += step;
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
-      chunk_step<T, D, NT, NPL, OFF64, APP>(rb[b], c + nw * b, false, step, cx, pv, qf, st,
-                                       bad_block, nr);
+      chunk_step<T, D, NT, NPL, OFF64, APP, KV8>(rb[b], c + nw * b, false, step, cx, pv, qf, st,
+                                                 bad_block, nr);
 }
 
 // Combination of the NW wavefronts' online-softmax states of one
@@ -473,7 +550,7 @@ __device__ __forceinline__ void put_new_row(char* lds, u32x4 piece, int tid) {
   if (tid < 2 * ChunkGeo<D>::CPR) *reinterpret_cast<u32x4*>(lds + tid * 16) = piece;
 }
 
-template <int D>
+template <typename T, int D, bool KV8>
 __device__ __forceinline__ void store_new_row(const char* lds, const AttnArgs& a, int s,
                                               int kvh, int pos, const int* tbl, int blk_lo,
                                               int nblk, int tid) {
@@ -494,8 +571,14 @@ __device__ __forceinline__ void store_new_row(const char* lds, const AttnArgs& a
   const bool is_v = tid >= Geo::CPR;
   const int64_t slot = (phys << a.bs_shift) + (pos & ((1 << a.bs_shift) - 1));
   char* pool = static_cast<char*>(const_cast<void*>(is_v ? a.v_pool : a.k_pool));
-  *reinterpret_cast<u32x4*>(pool + (slot * a.hkv + kvh) * D * 2 + (tid % Geo::CPR) * 16) =
-      *reinterpret_cast<const u32x4*>(lds + tid * 16);
+  const u32x4 piece = *reinterpret_cast<const u32x4*>(lds + tid * 16);
+  if constexpr (KV8) {
+    *reinterpret_cast<u32x2*>(pool + (slot * a.hkv + kvh) * D + (tid % Geo::CPR) * 8) =
+        narrow8<T>(piece);
+  } else {
+    *reinterpret_cast<u32x4*>(pool + (slot * a.hkv + kvh) * D * 2 + (tid % Geo::CPR) * 16) =
+        piece;
+  }
 }
 
 // Q^T fragments of one (token, kv head): head 16*nt + l16, dims of piece

@@ -23,6 +23,25 @@ inline int elem_bytes(int dtype) {
   return dtype == PKV_DTYPE_F32 ? 4 : 2;
 }
 
+// fp8 pools: the PKV_KV_FP8 flag of a dtype argument, and the element type
+// of Q / out / appended rows without it.
+inline bool dtype_kv8(int dtype) { return (dtype & PKV_KV_FP8) != 0; }
+inline int dtype_base(int dtype) { return dtype & ~PKV_KV_FP8; }
+
+// Nearest fp8 e4m3 value (OCP, torch.float8_e4m3fn: bias 7, 3 mantissa bits,
+// no infinities, S.1111.111 = NaN, largest finite 448) of x: ties to even;
+// |x| >= 480, infinities and NaN give NaN (0x7F with the sign bit); the
+// bytes torch's conversion gives. Values below 2^-6 are multiples of 2^-9.
+__device__ __forceinline__ unsigned f32_to_e4m3(float x) {
+  unsigned b = __float_as_uint(x);
+  const unsigned sign = (b >> 24) & 0x80u;
+  b &= 0x7fffffffu;
+  if (b >= 0x43F00000u) return sign | 0x7Fu;
+  if (b < 0x3C800000u) return sign | (unsigned)(int)rintf(__uint_as_float(b) * 512.f);
+  b += 0x7FFFFu + ((b >> 20) & 1u);  // 23 mantissa bits to 3, ties to even
+  return sign | ((((b >> 23) - 120u) << 3) | ((b >> 20) & 7u));
+}
+
 // x as an fp32 register value the compiler must produce before using it.
 // Without it the backend may fold an fp32 operation and the conversion to
 // fp16 that follows into one mixed-precision instruction (v_fma_mix*) that
@@ -61,6 +80,11 @@ int launch_append(void* k_pool, void* v_pool, int64_t pool_slots,
                   const void* k_new, const void* v_new, const int64_t* slots,
                   int64_t n_tok, int64_t row_bytes, int* status,
                   hipStream_t stream);
+// The same into fp8 pools: rows of row_elems values of src_dtype, each
+// rounded to fp8 (f32_to_e4m3).
+int launch_append_fp8(void* k_pool, void* v_pool, int64_t pool_slots, const void* k_new,
+                      const void* v_new, const int64_t* slots, int64_t n_tok,
+                      int64_t row_elems, int src_dtype, int* status, hipStream_t stream);
 
 int launch_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
                              int bs_shift, const void* k_new,
@@ -69,6 +93,13 @@ int launch_append_from_table(void* k_pool, void* v_pool, int64_t num_blocks,
                              const int32_t* start_pos, int n_seq,
                              int64_t n_tok, int64_t row_bytes, int min_qlen,
                              int* status, hipStream_t stream);
+
+int launch_append_from_table_fp8(void* k_pool, void* v_pool, int64_t num_blocks, int bs_shift,
+                                 const void* k_new, const void* v_new,
+                                 const int32_t* block_tables, int max_blk, const int32_t* qloc,
+                                 const int32_t* start_pos, int n_seq, int64_t n_tok,
+                                 int64_t row_elems, int src_dtype, int min_qlen, int* status,
+                                 hipStream_t stream);
 
 int launch_gather(void* k_out, void* v_out, const void* k_pool,
                   const void* v_pool, int64_t num_blocks, int bs_shift,
@@ -98,6 +129,7 @@ struct AttnArgs {
   int d;
   float scale_log2;  // softmax scale * log2(e)
   int causal;
+  int kv8;  // the pools hold fp8 e4m3 (q, out, k_new, v_new keep the 16-bit type)
   // which sequences this launch handles (a mixed batch is split between the
   // decode and the prefill kernels): 0 every one, 1 only those with one
   // query token, 2 only those with more

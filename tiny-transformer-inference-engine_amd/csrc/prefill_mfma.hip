@@ -35,7 +35,7 @@ using namespace mfma;
 constexpr int kPW = 8;             // wavefronts per workgroup
 constexpr int kPBlock = 64 * kPW;  // threads
 
-template <typename T, int D, int NT, int WPT, bool OFF64>
+template <typename T, int D, int NT, int WPT, bool OFF64, bool KV8>
 __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(AttnArgs a) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -97,8 +97,10 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
   const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
   const char* kbase = static_cast<const char*>(a.k_pool);
   const char* vbase = static_cast<const char*>(a.v_pool);
-  const int64_t row_stride = (int64_t)a.hkv * D * 2;
-  const int64_t head_off = (int64_t)kvh * D * 2;
+  const int64_t row_stride = (int64_t)a.hkv * D * (KV8 ? 1 : 2);
+  const int64_t head_off = (int64_t)kvh * D * (KV8 ? 1 : 2);
+  typedef typename PoolPiece<KV8>::type Piece;
+  constexpr int PB = PoolPiece<KV8>::kBytes;
   const int bs_mask = (1 << a.bs_shift) - 1;
   ChunkCtx cx;
   cx.tbl = tbl;
@@ -136,9 +138,9 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
     // two chunks are in flight while one is computed; issued for every
     // c < nch + 2 (past the end they re-read chunk nch - 1) so no load sits
     // under a branch.
-    u32x4 rgA[PER], rgB[PER];
+    Piece rgA[PER], rgB[PER];
     unsigned okA = 0, okB = 0;
-    auto issue = [&](int c, u32x4 (&rg)[PER], unsigned& okm) {
+    auto issue = [&](int c, Piece (&rg)[PER], unsigned& okm) {
       c = min(c, nch - 1);
       okm = 0;
 #pragma unroll
@@ -151,26 +153,31 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
         const int slotv = ((ok ? phys : 0) << a.bs_shift) + (pos & bs_mask);
         const char* base = is_v(k) ? vbase : kbase;
         if constexpr (OFF64) {
-          rg[k] = *reinterpret_cast<const u32x4*>(base + (int64_t)slotv * row_stride + head_off +
-                                                  pcol[k] * 16);
+          rg[k] = *reinterpret_cast<const Piece*>(base + (int64_t)slotv * row_stride + head_off +
+                                                  pcol[k] * PB);
         } else {
-          rg[k] = *reinterpret_cast<const u32x4*>(
+          rg[k] = *reinterpret_cast<const Piece*>(
               base + ((unsigned)slotv * (unsigned)row_stride + (unsigned)head_off +
-                      (unsigned)(pcol[k] * 16)));
+                      (unsigned)(pcol[k] * PB)));
         }
       }
     };
     // stage chunk c into LDS buffer c & 1 (free: every wavefront passed the
     // previous barrier after computing chunk c - 2), request chunk c + 2
     // into the same registers, then compute chunk c
-    auto step = [&](int c, u32x4 (&rg)[PER], unsigned& okm) {
+    auto step = [&](int c, Piece (&rg)[PER], unsigned& okm) {
       char* kl = buf[c & 1];
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
         const bool ok = (okm >> k) & 1;
         bad_block |= !ok;
+        u32x4 piece;
+        if constexpr (KV8)
+          piece = widen8<T>(rg[k]);
+        else
+          piece = rg[k];
         *reinterpret_cast<u32x4*>(kl + (is_v(k) ? Geo::BYTES : 0) + Geo::off(prow[k], pcol[k])) =
-            ok ? rg[k] : u32x4{0u, 0u, 0u, 0u};
+            ok ? piece : u32x4{0u, 0u, 0u, 0u};
       }
       issue(c + 2, rg, okm);
       __syncthreads();  // chunk c is staged; nobody reads the other buffer any more
@@ -212,12 +219,18 @@ template <typename T, int NT, int WPT, bool OFF64>
 int launch_nt(const AttnArgs& a, hipStream_t stream) {
   constexpr int tq = kPW / WPT;
   const dim3 grid((a.n_tokens + tq - 1) / tq + a.n_seq, a.hkv);
-  if (a.d == 64)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, NT, WPT, OFF64>), grid, dim3(kPBlock), 0,
-                       stream, a);
+  if (a.d == 64 && a.kv8)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, NT, WPT, OFF64, true>), grid, dim3(kPBlock),
+                       0, stream, a);
+  else if (a.d == 64)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, NT, WPT, OFF64, false>), grid, dim3(kPBlock),
+                       0, stream, a);
+  else if (a.d == 128 && a.kv8)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, NT, WPT, OFF64, true>), grid, dim3(kPBlock),
+                       0, stream, a);
   else if (a.d == 128)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, NT, WPT, OFF64>), grid, dim3(kPBlock), 0,
-                       stream, a);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, NT, WPT, OFF64, false>), grid,
+                       dim3(kPBlock), 0, stream, a);
   else
     return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: d=%d", a.d);
   return check_launch("prefill_mfma_kernel");

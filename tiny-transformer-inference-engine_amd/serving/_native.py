@@ -17,6 +17,10 @@ _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libpagedkv.so")
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+# OR-ed into a dtype code: the K/V pools hold fp8 e4m3 (torch.float8_e4m3fn)
+# while Q, out and appended rows keep the coded type
+PKV_KV_FP8 = 0x100
+FP8_KV_DTYPE = torch.float8_e4m3fn
 
 PKV_ERR_INVALID = -1
 PKV_ERR_UNSUPPORTED = -2
@@ -157,6 +161,17 @@ def dtype_code(dtype: torch.dtype) -> int:
         return DTYPE_CODES[dtype]
     except KeyError:
         raise TypeError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16")
+
+
+def kv_code(q_dtype: torch.dtype, pool_dtype: torch.dtype) -> int:
+    """dtype argument of a call with Q (or appended rows) of q_dtype and pools
+    of pool_dtype: pools share the 16/32-bit type, or are fp8 e4m3."""
+    if pool_dtype == FP8_KV_DTYPE:
+        return dtype_code(q_dtype) | PKV_KV_FP8
+    if pool_dtype != q_dtype:
+        raise TypeError(f"pool dtype {pool_dtype} with rows of {q_dtype}: pools share the "
+                        "rows' dtype or are float8_e4m3fn")
+    return dtype_code(q_dtype)
 
 
 def stream_ptr(device: torch.device) -> int:

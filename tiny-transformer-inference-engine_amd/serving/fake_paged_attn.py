@@ -57,7 +57,7 @@ def _launch(q, k_pool, v_pool, block_tables, seq_lens, queryloc, n_seq,
     T, hq, d = q.shape
     nb, bs, hkv, _ = k_pool.shape
     max_blk = block_tables.shape[1] if block_tables.dim() == 2 else 0
-    code = _native.dtype_code(q.dtype)
+    code = _native.kv_code(q.dtype, k_pool.dtype)
     L = _native.lib()
     ws_bytes = L.pkv_attention_workspace_bytes(
         n_seq, max_q_len, hq, hkv, d, max_blk, bs, max_kv_len, part_tokens, code)
@@ -232,7 +232,9 @@ def paged_attention_append_meta(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
     v = v.contiguous()
     T, hq, d = q.shape
     kp, vp = pool.flat_k[layer], pool.flat_v[layer]
-    code = _native.dtype_code(q.dtype)
+    if k.dtype != q.dtype:
+        raise TypeError(f"new K/V rows ({k.dtype}) must have the queries' dtype ({q.dtype})")
+    code = _native.kv_code(q.dtype, pool.dtype)
     L = _native.lib()
     max_blk = meta.block_tables.shape[1] if meta.block_tables.dim() == 2 else 0
     ws_bytes = L.pkv_attention_workspace_bytes(

@@ -65,6 +65,15 @@ class KVPool:
             device=device,
         )
 
+    @classmethod
+    def from_engine_config(cls, ecfg, device):
+        """A pool for an EngineConfig: the model's layers and heads, the
+        cache's block size and block count, kv_dtype (fp8 with
+        CacheConfig.kv_dtype = torch.float8_e4m3fn)."""
+        m = ecfg.model
+        return cls(m.num_layers, ecfg.cache.block_size, ecfg.num_blocks, m.num_kv_heads,
+                   m.head_dim, ecfg.kv_dtype, device)
+
     def _shape_check(self):
         expected = (self.num_layers, 2, self.num_blocks, self.block_size,
                     self.num_kv_heads, self.head_dim)
@@ -124,8 +133,7 @@ class KVPool:
             f"k has {k.shape[0]} rows but slot_mapping has {slot_mapping.numel()} slots"
         assert k.shape[1:] == (self.num_kv_heads, self.head_dim), \
             f"k trailing dims {k.shape[1:]} != expected {(self.num_kv_heads, self.head_dim)}"
-        assert k.dtype == self.dtype, f"k dtype {k.dtype} != pool dtype {self.dtype}"
-        assert v.dtype == self.dtype, f"v dtype {v.dtype} != pool dtype {self.dtype}"
+        self._check_row_dtype(k, v)
 
         _native.require_device(self.kv, k, v, slot_mapping, what="KVPool.write")
         if k.device != self.device or v.device != self.device:
@@ -137,18 +145,28 @@ class KVPool:
         rc = _native.lib().pkv_append(
             self.flat_k[layer].data_ptr(), self.flat_v[layer].data_ptr(), self.num_slots,
             k.data_ptr(), v.data_ptr(), slots.data_ptr(), k.shape[0],
-            self.num_kv_heads * self.head_dim, _native.dtype_code(self.dtype),
+            self.num_kv_heads * self.head_dim, _native.kv_code(k.dtype, self.dtype),
             _native.ptr(status), _native.stream_ptr(self.device))
         _native.check(rc, "pkv_append")
         self._raise_status(status, "KVPool.write")
+
+    def _check_row_dtype(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Rows of the pool's dtype; an fp8 pool (kv_dtype float8_e4m3fn)
+        takes float32/float16/bfloat16 rows and rounds them on the way in,
+        as the reference's index_put into a float8 pool does."""
+        if self.dtype == _native.FP8_KV_DTYPE:
+            assert k.dtype == v.dtype and k.dtype in _native.DTYPE_CODES, \
+                f"k/v dtype {k.dtype}/{v.dtype}: an fp8 pool takes float32, float16 or bfloat16 rows"
+        else:
+            assert k.dtype == self.dtype, f"k dtype {k.dtype} != pool dtype {self.dtype}"
+            assert v.dtype == self.dtype, f"v dtype {v.dtype} != pool dtype {self.dtype}"
 
     def check_rows(self, k: torch.Tensor, v: torch.Tensor, meta) -> None:
         """The checks of KVPool.write (kv_pool.py:58-67) for a step's rows."""
         assert k.shape == v.shape, f"k/v shape mismatch: {k.shape} vs {v.shape}"
         assert k.shape[1:] == (self.num_kv_heads, self.head_dim), \
             f"k trailing dims {k.shape[1:]} != expected {(self.num_kv_heads, self.head_dim)}"
-        assert k.dtype == self.dtype and v.dtype == self.dtype, \
-            f"k/v dtype {k.dtype}/{v.dtype} != pool dtype {self.dtype}"
+        self._check_row_dtype(k, v)
         assert k.shape[0] == meta.num_tokens, \
             f"k has {k.shape[0]} rows but the batch has {meta.num_tokens} tokens"
 
@@ -166,7 +184,7 @@ class KVPool:
             self.block_size, k.data_ptr(), v.data_ptr(), meta.block_tables.data_ptr(),
             meta.max_blocks, meta.query_start_loc.data_ptr(), meta.start_pos.data_ptr(),
             meta.num_seqs, k.shape[0], self.num_kv_heads * self.head_dim,
-            _native.dtype_code(self.dtype), _native.ptr(status),
+            _native.kv_code(k.dtype, self.dtype), _native.ptr(status),
             _native.stream_ptr(self.device))
         _native.check(rc, "pkv_append_from_table")
         self._raise_status(status, "KVPool.write_from_table")
@@ -174,6 +192,11 @@ class KVPool:
     # ------------------------------------------------------------------
     # gather
     # ------------------------------------------------------------------
+    def _gather_code(self) -> int:
+        if self.dtype == _native.FP8_KV_DTYPE:
+            return _native.DTYPE_CODES[torch.bfloat16] | _native.PKV_KV_FP8  # byte copy
+        return _native.dtype_code(self.dtype)
+
     def gather(self, layer: int, block_table: list[int], seq_len: int):
         """Dense copy of one sequence's first seq_len rows (kv_pool.py:72-82)."""
         assert seq_len <= len(block_table) * self.block_size, \
@@ -186,7 +209,7 @@ class KVPool:
         rc = _native.lib().pkv_gather(
             k.data_ptr(), v.data_ptr(), self.kv[layer, 0].data_ptr(), self.kv[layer, 1].data_ptr(),
             self.num_blocks, self.block_size, bt.data_ptr(), bt.numel(), seq_len,
-            self.num_kv_heads * self.head_dim, _native.dtype_code(self.dtype),
+            self.num_kv_heads * self.head_dim, self._gather_code(),
             _native.ptr(status), _native.stream_ptr(self.device))
         _native.check(rc, "pkv_gather")
         self._raise_status(status, "KVPool.gather")

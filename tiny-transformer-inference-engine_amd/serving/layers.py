@@ -170,6 +170,53 @@ class ModelConfig:
 
 
 @dataclass
+class CacheConfig:
+    """KV cache settings (reference: models/model_config.py:45-51). kv_dtype
+    None means the model's dtype; torch.float8_e4m3fn gives fp8 pools (new
+    rows rounded on append, widened exactly by the attention kernels)."""
+    block_size: int = 16
+    num_gpu_blocks: int | None = None
+    kv_budget_bytes: int = 2 * 1024**3
+    kv_dtype: torch.dtype | None = None
+    enable_prefix_caching: bool = False
+
+
+@dataclass
+class EngineConfig:
+    """Model + cache + scheduler settings with the derived pool geometry
+    (reference: models/model_config.py:73-100)."""
+    model: ModelConfig = field(default_factory=ModelConfig)
+    cache: CacheConfig = field(default_factory=CacheConfig)
+    sched: "SchedulerConfig" = field(default_factory=lambda: SchedulerConfig())
+
+    @property
+    def kv_dtype(self) -> torch.dtype:
+        return self.cache.kv_dtype or self.model.dtype
+
+    @property
+    def max_blocks_per_seq(self) -> int:
+        return -(-self.model.max_seq_len // self.cache.block_size)
+
+    @property
+    def bytes_per_block(self) -> int:
+        m, c = self.model, self.cache
+        elem = torch.empty((), dtype=self.kv_dtype).element_size()
+        return 2 * m.num_layers * c.block_size * m.num_kv_heads * m.head_dim * elem
+
+    @property
+    def num_blocks(self) -> int:
+        n = self.cache.num_gpu_blocks
+        return n if n is not None else self.cache.kv_budget_bytes // self.bytes_per_block
+
+    def __post_init__(self):
+        bs = self.cache.block_size
+        assert bs & (bs - 1) == 0, "block_size must be a power of two"
+        if not self.sched.enable_chunked_prefill:
+            assert self.sched.max_num_batched_tokens >= self.model.max_seq_len, \
+                "without chunked prefill, a full-length prompt must fit in one step"
+
+
+@dataclass
 class SchedulerConfig:
     """Scheduler limits (reference: models/model_config.py:56-70, where the
     fields exist but the reference scheduler does not read them; here
