@@ -32,31 +32,11 @@ using namespace mfma;
 constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
 
-// chunks of virtual sequence v (= sequence * hkv + kv head): 0 when the
-// sequence has no query this step, at least 1 otherwise (an empty context
-// still owes a zero row and lse = +inf)
-__device__ __forceinline__ int sk_chunks(const AttnArgs& a, int v, int& kv_len) {
-  const int s = v / a.hkv;
-  kv_len = 0;
-  if (a.qloc) {
-    const int q0 = a.qloc[s];
-    const int ql = a.qloc[s + 1] - q0;
-    if (ql <= 0 || (a.qfilter == 1 && ql != 1)) return 0;
-    if (q0 < 0 || q0 + ql > a.n_tokens) {
-      if (a.status) atomicOr(a.status, PKV_STATUS_BAD_QLOC);
-      return 0;
-    }
-  }
-  int kl = a.seq_lens[s];
-  const int cap = a.max_blk << a.bs_shift;
-  kl = kl < cap ? kl : cap;
-  kv_len = kl > 0 ? kl : 0;
-  return kv_len > 0 ? (kv_len + kChunk - 1) / kChunk : 1;
-}
-
-// chunks and clamped context of one sequence, as sk_chunks, from its
-// query_start_loc pair (q0, q1; 0, 1 without query_start_loc) and seq_len
-// (a malformed pair has been flagged by the scan's sk_chunks)
+// Chunks of virtual sequence v (= sequence * hkv + kv head) and its clamped
+// context, from its query_start_loc pair (q0, q1; 0, 1 without
+// query_start_loc) and seq_len: 0 chunks when the sequence has no query this
+// step, at least 1 otherwise (an empty context still owes a zero row and
+// lse = +inf); a malformed pair has been flagged by the scan (scan_desc)
 struct SeqDesc {
   int n, kv_len;
 };
@@ -81,6 +61,29 @@ __device__ __forceinline__ SeqDesc load_desc(const AttnArgs& a, int v, const int
   const int q0 = ld_meta(qsrc, s);
   const int q1 = ld_meta(qsrc, s + 1);
   return seq_desc(a, a.qloc ? q0 : 0, a.qloc ? q1 : 1, kl);
+}
+
+// The scan's view of pair v: its three metadata loads issued together
+// (vector loads, one round trip) and its query token; a malformed query
+// range is flagged once (by workgroup 0).
+struct ScanDesc {
+  SeqDesc d;
+  int q0;  // first query token (its row of q / out)
+};
+__device__ __forceinline__ ScanDesc scan_desc(const AttnArgs& a, int v, const int32_t* alt) {
+  const int s = v / a.hkv;
+  const int32_t* qsrc = a.qloc ? a.qloc : alt;
+  const int kl = a.seq_lens[s];
+  const int q0 = qsrc[s];
+  const int q1 = qsrc[a.qloc ? s + 1 : s];
+  ScanDesc r;
+  r.q0 = a.qloc ? q0 : s;
+  const int ql = a.qloc ? q1 - q0 : 1;
+  if (a.qloc && ql > 0 && !(a.qfilter == 1 && ql != 1) && (q0 < 0 || q0 + ql > a.n_tokens) &&
+      a.status && blockIdx.x == 0)
+    atomicOr(a.status, PKV_STATUS_BAD_QLOC);
+  r.d = seq_desc(a, r.q0, a.qloc ? q1 : s + 1, kl);
+  return r;
 }
 
 // first chunk of workgroup w's share, and the workgroup owning chunk x
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   __shared__ float ml_lds[kWaves][G][2];
   __shared__ int tbl[kTblCap];
   __shared__ int scan_sh[kBlock];
-  __shared__ int s_v0, s_g0, s_last;
+  __shared__ int s_v0, s_g0, s_last, s_n0, s_kl0, s_q0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -223,13 +226,16 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   const int K = k.seg_cost;
   int C = 0;
   int n_mine = 0, ex_mine = 0;
+  ScanDesc sd_mine{};
+  const int32_t* alt = reinterpret_cast<const int32_t*>(k.recs);
   for (int base = 0; base < V; base += kBlock) {
-    int kl;
-    const int n = base + tid < V ? sk_cost(sk_chunks(a, base + tid, kl), K) : 0;
+    const ScanDesc sd = scan_desc(a, min(base + tid, V - 1), alt);
+    const int n = base + tid < V ? sk_cost(sd.d.n, K) : 0;
     int ex;
     C += block_scan(n, scan_sh, ex);
     n_mine = n;
     ex_mine = ex;
+    sd_mine = sd;
   }
   // at most one share per unit, so that every share is non-empty
   const int W = k.n_wg < C ? k.n_wg : C;
@@ -238,22 +244,30 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   const int end = share_start(wg + 1, C, W);
   if (tid == 0) s_v0 = -1;
   __syncthreads();
+  // the pair whose interval holds the share's start, with its metadata (so
+  // the segment loop starts without reloading it)
   if (V <= kBlock) {
     if (n_mine > 0 && ex_mine <= start && start < ex_mine + n_mine) {
       s_v0 = tid;
       s_g0 = ex_mine;
+      s_n0 = sd_mine.d.n;
+      s_kl0 = sd_mine.d.kv_len;
+      s_q0 = sd_mine.q0;
     }
   } else {
     int run = 0;
     for (int base = 0; base < V; base += kBlock) {
-      int kl;
       const int v = base + tid;
-      const int n = v < V ? sk_cost(sk_chunks(a, v, kl), K) : 0;
+      const ScanDesc sd = scan_desc(a, min(v, V - 1), alt);
+      const int n = v < V ? sk_cost(sd.d.n, K) : 0;
       int ex;
       const int tot = block_scan(n, scan_sh, ex);
       if (n > 0 && run + ex <= start && start < run + ex + n) {
         s_v0 = v;
         s_g0 = run + ex;
+        s_n0 = sd.d.n;
+        s_kl0 = sd.d.kv_len;
+        s_q0 = sd.q0;
       }
       run += tot;
       __syncthreads();
@@ -288,11 +302,13 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   // uniform across the workgroup: scalar registers for the segment loop
   int v = __builtin_amdgcn_readfirstlane(s_v0);
   int g0 = __builtin_amdgcn_readfirstlane(s_g0);  // cost position where v's interval starts
-  SeqDesc dsc = load_desc(a, v, reinterpret_cast<const int32_t*>(k.recs));  // n > 0: the share's start lies in v's chunks
+  SeqDesc dsc;  // n > 0: the share's start lies in v's chunks
+  dsc.n = __builtin_amdgcn_readfirstlane(s_n0);
+  dsc.kv_len = __builtin_amdgcn_readfirstlane(s_kl0);
   v8 qf[NT][D / 32];
   {
     const int s = v / a.hkv;
-    const int qtok = a.qloc ? ld_meta(a.qloc, s) : s;
+    const int qtok = __builtin_amdgcn_readfirstlane(s_q0);
     load_q<T, D, NT>(qf, q, (int64_t)qtok * a.hq + (v - s * a.hkv) * G, grp, l16);
   }
   bool first = true;
