@@ -111,6 +111,29 @@ def test_shim_append_and_attend_matches_oracle():
     check(out[pick], exp, "append_and_attend")
 
 
+def test_shim_fp8_pools():
+    """The shim with float8_e4m3fn pools (CacheConfig.kv_dtype): KVPool.write
+    body as INTEGRATION.md gives it is not exercised here (the product's
+    KVPool is), but both attention stubs are: paged_attn_fwd on a cfg5-shaped
+    batch with fp8 pools, against the oracle on the pools' fp8 values."""
+    print("[shim] fp8 pools", flush=True)
+    ns = shim_namespace()
+    dev = torch.device(DEV)
+    p = workloads.cfg5_problem(dev, seed=4, bs=16)
+    k8, v8 = p.k_pool.to(torch.float8_e4m3fn), p.v_pool.to(torch.float8_e4m3fn)
+    n = p.n_seq
+    qloc = torch.arange(n + 1, dtype=torch.int32, device=DEV)
+    O, lse = ns["paged_attn_fwd"](p.q, k8, v8, p.block_tables, p.seq_lens, qloc, 1)
+    torch.cuda.synchronize()
+    order = np.argsort(-p.lens)
+    pick = sorted(set(order[:4].tolist()) | set(range(0, n, max(1, n // 6))))
+    kv = [ref.e4m3_values(t.view(torch.uint8).cpu().numpy()) for t in (k8, v8)]
+    exp, exp_lse = ref.paged_attention(np64(p.q[pick]), kv[0], kv[1],
+                                       p.block_tables[pick].cpu().numpy(), p.lens[pick], None)
+    check(O[pick], exp, "fp8 pools")
+    assert np.abs(lse[pick].cpu().numpy() - exp_lse).max() < 2e-2
+
+
 @pytest.mark.parametrize("part", [0, _native.PART_PERSISTENT])
 def test_dirty_workspace_is_reported(part):
     """A workspace allocated without zero-filling (here: every byte 7) makes
