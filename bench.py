@@ -632,6 +632,10 @@ def run_profile(args, torch):
         args.warmup = 1
         run_model(args, torch)
         return
+    if args.profile in ("cfg1", "cfg2"):
+        args.steps = args.profile_iters
+        (run_cfg1 if args.profile == "cfg1" else run_cfg2)(args, torch)
+        return
     if args.profile == "sampling":
         from serving import fused_ops
         g = torch.Generator(device=dev).manual_seed(0)
@@ -707,8 +711,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
-    ap.add_argument("--profile", choices=["cfg4", "cfg4step", "cfg5", "cfg5mixed", "model",
-                                          "sampling"], default=None,
+    ap.add_argument("--profile", choices=["cfg1", "cfg2", "cfg4", "cfg4step", "cfg5", "cfg5mixed",
+                                          "model", "sampling"], default=None,
                     help="run only the launches of this workload (a rocprofv3 target); "
                          "no JSON line")
     ap.add_argument("--profile-iters", type=int, default=20)
