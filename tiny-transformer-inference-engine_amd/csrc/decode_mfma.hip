@@ -33,7 +33,7 @@ static_assert(kBlock >= kTblCap, "one thread per table entry of a window");
 // per SIMD the register budget is sized for; APP = the fused append of
 // a.k_new / a.v_new at a.new_pos (compiled out of the plain attention); KV8 =
 // fp8 pools (rows widened to T when staged in LDS).
-template <typename T, int D, int NT, int PF, int OCC, bool OFF64, bool APP, bool KV8>
+template <typename T, int D, int NT, int PF, int OCC, bool HALVES, bool APP, bool KV8>
 __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   __shared__ int tbl[kTblCap];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
   const int grp = lane >> 4;
   const int l16 = lane & 15;
   const int part = blockIdx.y;
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
       for (int i = threadIdx.x; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
     }
     __syncthreads();
-    run_chunks<T, D, NT, PF, OFF64, APP, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+    run_chunks<T, D, NT, PF, HALVES, APP, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
     last_blk_lo = cx.blk_lo;
     last_nblk = nblk;
   }
@@ -290,38 +290,38 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
-// <T, D, NT, PF, OCC, OFF64, APP, KV8>: two wavefronts per SIMD
-template <typename T, int D, int NT, int PF, bool OFF64, bool KV8>
+// <T, D, NT, PF, OCC, HALVES, APP, KV8>: two wavefronts per SIMD
+template <typename T, int D, int NT, int PF, bool HALVES, bool KV8>
 void launch_k(const AttnArgs& a, dim3 grid, hipStream_t stream) {
   if (a.new_pos)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, true, KV8>), grid,
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, HALVES, true, KV8>), grid,
                        dim3(kBlock), 0, stream, a);
   else
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, OFF64, false, KV8>), grid,
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, HALVES, false, KV8>), grid,
                        dim3(kBlock), 0, stream, a);
 }
-template <typename T, int D, int NT, int PF, bool OFF64>
+template <typename T, int D, int NT, int PF, bool HALVES>
 void launch_v(const AttnArgs& a, dim3 grid, hipStream_t stream) {
   if (a.kv8)
-    launch_k<T, D, NT, PF, OFF64, true>(a, grid, stream);
+    launch_k<T, D, NT, PF, HALVES, true>(a, grid, stream);
   else
-    launch_k<T, D, NT, PF, OFF64, false>(a, grid, stream);
+    launch_k<T, D, NT, PF, HALVES, false>(a, grid, stream);
 }
 
-template <typename T, bool OFF64>
+template <typename T, bool HALVES>
 int launch_t(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
   const dim3 grid(a.n_seq * a.hkv, p.parts_max);
   const int nt = a.group / 16;
   // the D = 128 variants have room for one chunk in flight per wavefront,
   // the D = 64 ones for two
   if (a.d == 64 && nt == 1)
-    launch_v<T, 64, 1, 2, OFF64>(a, grid, stream);
+    launch_v<T, 64, 1, 2, HALVES>(a, grid, stream);
   else if (a.d == 64 && nt == 2)
-    launch_v<T, 64, 2, 2, OFF64>(a, grid, stream);
+    launch_v<T, 64, 2, 2, HALVES>(a, grid, stream);
   else if (a.d == 128 && nt == 1)
-    launch_v<T, 128, 1, 1, OFF64>(a, grid, stream);
+    launch_v<T, 128, 1, 1, HALVES>(a, grid, stream);
   else if (a.d == 128 && nt == 2)
-    launch_v<T, 128, 2, 1, OFF64>(a, grid, stream);
+    launch_v<T, 128, 2, 1, HALVES>(a, grid, stream);
   else
     return fail(PKV_ERR_UNSUPPORTED, "decode_mfma: d=%d group=%d", a.d, a.group);
   return check_launch("decode_mfma_kernel");
@@ -344,11 +344,14 @@ int launch_decode_mfma(const AttnArgs& a, const AttnPlan& p, int dtype,
                        hipStream_t stream) {
   if (a.num_blocks >= (int64_t(1) << 31))
     return fail(PKV_ERR_UNSUPPORTED, "decode_mfma: %lld blocks", (long long)a.num_blocks);
-  const bool off64 = pool_needs_off64(a);
+  // blocks of 16 tokens or more: per-half chunk addressing (every chunk
+  // starts 16-aligned: partitions, shares and table windows are multiples
+  // of 32 tokens or of the block size)
+  const bool halves = a.bs_shift >= 4;
   if (dtype == PKV_DTYPE_BF16)
-    return off64 ? launch_t<bf16, true>(a, p, stream) : launch_t<bf16, false>(a, p, stream);
+    return halves ? launch_t<bf16, true>(a, p, stream) : launch_t<bf16, false>(a, p, stream);
   if (dtype == PKV_DTYPE_F16)
-    return off64 ? launch_t<f16, true>(a, p, stream) : launch_t<f16, false>(a, p, stream);
+    return halves ? launch_t<f16, true>(a, p, stream) : launch_t<f16, false>(a, p, stream);
   return fail(PKV_ERR_UNSUPPORTED, "decode_mfma: dtype %d", dtype);
 }
 

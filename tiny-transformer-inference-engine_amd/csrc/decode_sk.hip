@@ -196,7 +196,7 @@ __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, in
   if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
-template <typename T, int D, int NT, int PF, bool OFF64, bool KV8>
+template <typename T, int D, int NT, int PF, bool HALVES, bool KV8>
 __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs k) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int grp = lane >> 4;
   const int l16 = lane & 15;
   const int wg = blockIdx.x;
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
         for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
       }
       __syncthreads();
-      run_chunks<T, D, NT, PF, OFF64, false, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+      run_chunks<T, D, NT, PF, HALVES, false, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
     }
 
     // ---- the next segment: its Q and first table window are loaded now
@@ -491,27 +491,27 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
 }
 
-template <typename T, int D, int NT, int PF, bool OFF64>
+template <typename T, int D, int NT, int PF, bool HALVES>
 int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
   k.n_wg = sk_workgroups(D, 16 * NT);
   if (a.kv8)
-    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, true>), dim3(k.n_wg), dim3(kBlock),
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, true>), dim3(k.n_wg), dim3(kBlock),
                        0, stream, a, k);
   else
-    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, OFF64, false>), dim3(k.n_wg),
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, false>), dim3(k.n_wg),
                        dim3(kBlock), 0, stream, a, k);
   return check_launch("decode_sk_kernel");
 }
 
-template <typename T, bool OFF64>
+template <typename T, bool HALVES>
 int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
   const int nt = a.group / 16;
-  // <T, D, NT, PF, OFF64>: two wavefronts per SIMD; the D = 128 variants
+  // <T, D, NT, PF, HALVES>: two wavefronts per SIMD; the D = 128 variants
   // have room for one chunk in flight per wavefront, the D = 64 ones for two
-  if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, OFF64>(a, k, stream);
-  if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, OFF64>(a, k, stream);
-  if (a.d == 128 && nt == 1) return launch_v<T, 128, 1, 1, OFF64>(a, k, stream);
-  if (a.d == 128 && nt == 2) return launch_v<T, 128, 2, 1, OFF64>(a, k, stream);
+  if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, HALVES>(a, k, stream);
+  if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, HALVES>(a, k, stream);
+  if (a.d == 128 && nt == 1) return launch_v<T, 128, 1, 1, HALVES>(a, k, stream);
+  if (a.d == 128 && nt == 2) return launch_v<T, 128, 2, 1, HALVES>(a, k, stream);
   return fail(PKV_ERR_UNSUPPORTED, "decode_sk: d=%d group=%d", a.d, a.group);
 }
 
@@ -527,11 +527,14 @@ int sk_workgroups(int d, int group) {
 int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream) {
   if (a.num_blocks >= (int64_t(1) << 31))
     return fail(PKV_ERR_UNSUPPORTED, "decode_sk: %lld blocks", (long long)a.num_blocks);
-  const bool off64 = pool_needs_off64(a);
+  // blocks of 16 tokens or more: per-half chunk addressing (every chunk
+  // starts 16-aligned: partitions, shares and table windows are multiples
+  // of 32 tokens or of the block size)
+  const bool halves = a.bs_shift >= 4;
   if (dtype == PKV_DTYPE_BF16)
-    return off64 ? launch_t<bf16, true>(a, k, stream) : launch_t<bf16, false>(a, k, stream);
+    return halves ? launch_t<bf16, true>(a, k, stream) : launch_t<bf16, false>(a, k, stream);
   if (dtype == PKV_DTYPE_F16)
-    return off64 ? launch_t<f16, true>(a, k, stream) : launch_t<f16, false>(a, k, stream);
+    return halves ? launch_t<f16, true>(a, k, stream) : launch_t<f16, false>(a, k, stream);
   return fail(PKV_ERR_UNSUPPORTED, "decode_sk: dtype %d", dtype);
 }
 

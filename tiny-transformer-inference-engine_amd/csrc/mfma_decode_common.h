@@ -116,6 +116,11 @@ constexpr int kTblCap = 256;  // block-table entries staged in LDS at a time
 constexpr float kLazy = 8.f;  // log2 headroom of the lazily moved softmax reference
 constexpr float kLn2f = 0.6931471805599453f;
 
+// 2^x by the hardware's v_exp_f32 alone (the library exp2f adds a rescaling
+// for results below 2^-126). Softmax weights that small are below bf16/fp16
+// resolution next to the weight-1 term every row holds; -inf gives 0.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // LDS geometry of one 32-token chunk of K (or V) rows, D bf16/fp16 each.
 // Rows are padded by 16 bytes (PITCH = 2D + 16): row r starts 4r (mod 64)
 // banks further on for D = 128 (36r for D = 64), so the 16 rows an MFMA
@@ -171,13 +176,34 @@ struct ChunkCtx {
 };
 
 // Branch-free loads of chunk `c` (tokens seg_lo + 32c ...): rows past
-// seg_hi re-read the range's last row (their scores are masked to -inf, so
+// seg_hi re-read rows inside the range (their scores are masked to -inf, so
 // they contribute exactly 0); rows whose table entry is outside the pool
 // read block 0 and are zeroed when staged. Nothing here consumes a load
 // result, so the loads stay in flight until the chunk is staged.
-// OFF64 = false when every byte offset of the pool fits in 31 bits: the load
-// is then a uniform base plus a 32-bit per-lane offset.
-template <class Geo, int NPL, bool OFF64, bool KV8>
+//
+// HALVES (block size >= 16, chunk starts 16-aligned): each 16-row half of
+// the chunk lies in one block, so a half costs one table read and is read
+// through a buffer resource of its own (uniform: base = the half's first
+// row, size = 16 rows, or 0 for a bad table entry, which makes every load of
+// the half return zeros without touching memory); each lane adds only its
+// row and piece offset (one min and one multiply-add per load). A half that
+// lies wholly past seg_hi re-reads the first half. Otherwise every row
+// reads its own table entry and forms a 64-bit address, and bad rows are
+// zeroed when staged.
+template <bool KV8>
+__device__ __forceinline__ typename PoolPiece<KV8>::type load_piece(__amdgpu_buffer_rsrc_t rs,
+                                                                    unsigned off) {
+  constexpr int kNonTemporal = 2;
+  if constexpr (KV8)
+    return __builtin_bit_cast(u32x2,
+                              __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kNonTemporal));
+  else
+    return __builtin_bit_cast(u32x4,
+                              __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kNonTemporal));
+}
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) dword buffer, gfx9 family
+
+template <class Geo, int NPL, bool HALVES, bool KV8>
 __device__ __forceinline__ void load_chunk(ChunkRegs<NPL, KV8>& r, const PoolView& pv,
                                            const ChunkCtx& cx, int c) {
   typedef typename PoolPiece<KV8>::type P;
@@ -185,22 +211,43 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NPL, KV8>& r, const PoolVie
   const int bs_mask = (1 << pv.bs_shift) - 1;
   const int cb = cx.seg_lo + c * kChunk;
   unsigned vmask = 0;
+  if constexpr (HALVES) {
+    constexpr int LPH = NPL / 2;  // loads per 16-row half
+    static_assert(LPH * Geo::ROWS_PER_LOAD == 16, "a half is 16 rows");
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) {
-    int pos = cb + cx.prow + j * Geo::ROWS_PER_LOAD;
-    pos = pos < cx.seg_hi ? pos : cx.seg_hi - 1;
-    pos = pos > 0 ? pos : 0;  // an empty context (seg_hi = 0) reads row 0
-    const int phys = cx.tbl[(pos >> pv.bs_shift) - cx.blk_lo];
-    const bool ok = (unsigned)phys < (unsigned)pv.num_blocks;
-    vmask |= (unsigned)ok << j;
-    const int slot = ((ok ? phys : 0) << pv.bs_shift) + (pos & bs_mask);
-    if constexpr (OFF64) {
-      const int64_t off = (int64_t)slot * pv.row_stride + pv.head_off + cx.pcol * PB;
-      r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.kbase + off));
-      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.vbase + off));
-    } else {
-      const unsigned off = (unsigned)slot * (unsigned)pv.row_stride +
-                           (unsigned)pv.head_off + (unsigned)(cx.pcol * PB);
+    for (int h = 0; h < 2; ++h) {
+      const int hs = cb + 16 * h < cx.seg_hi ? cb + 16 * h : cb;
+      const int lim = max(0, min(15, cx.seg_hi - 1 - hs));  // last row of the half in range
+      const int phys = __builtin_amdgcn_readfirstlane(cx.tbl[(hs >> pv.bs_shift) - cx.blk_lo]);
+      const bool ok = (unsigned)phys < (unsigned)pv.num_blocks;
+      const int64_t base =
+          ((((int64_t)(ok ? phys : 0)) << pv.bs_shift) + (hs & bs_mask)) * pv.row_stride +
+          pv.head_off;
+      const int extent = ok ? 16 * (int)pv.row_stride : 0;
+      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(pv.kbase + base), (short)0, extent, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(pv.vbase + base), (short)0, extent, kRsrcWord3);
+#pragma unroll
+      for (int j = 0; j < LPH; ++j) {
+        const int row = min(cx.prow + j * Geo::ROWS_PER_LOAD, lim);
+        const unsigned off = (unsigned)row * (unsigned)pv.row_stride + (unsigned)(cx.pcol * PB);
+        r.k[h * LPH + j] = load_piece<KV8>(kr, off);
+        r.v[h * LPH + j] = load_piece<KV8>(vr, off);
+      }
+      vmask |= (ok ? (1u << LPH) - 1 : 0u) << (h * LPH);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      int pos = cb + cx.prow + j * Geo::ROWS_PER_LOAD;
+      pos = pos < cx.seg_hi ? pos : cx.seg_hi - 1;
+      pos = pos > 0 ? pos : 0;  // an empty context (seg_hi = 0) reads row 0
+      const int phys = cx.tbl[(pos >> pv.bs_shift) - cx.blk_lo];
+      const bool ok = (unsigned)phys < (unsigned)pv.num_blocks;
+      vmask |= (unsigned)ok << j;
+      const int64_t slot = ((int64_t)(ok ? phys : 0) << pv.bs_shift) + (pos & bs_mask);
+      const int64_t off = slot * pv.row_stride + pv.head_off + cx.pcol * PB;
       r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.kbase + off));
       r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const P*>(pv.vbase + off));
     }
@@ -278,16 +325,19 @@ __device__ __forceinline__ void stage_new_row(const NewRow& nr, int cb, const Ch
 
 // Registers -> this wavefront's LDS slice, widened to T from an fp8 pool
 // (rows with a bad table entry are zeroed and flagged).
-template <typename T, class Geo, int NPL, bool KV8>
+// ZEROED: the loads already returned zeros for bad rows (HALVES loads).
+template <typename T, class Geo, int NPL, bool KV8, bool ZEROED>
 __device__ __forceinline__ void stage_chunk(const ChunkRegs<NPL, KV8>& r, const ChunkCtx& cx,
                                             bool& bad_block) {
   asm volatile("" ::: "memory");
+  constexpr unsigned kAll = (1u << NPL) - 1;
+  if constexpr (ZEROED) bad_block |= r.valid != kAll;
+  // every row valid (the rule) on every lane: plain stores, no selects
+  const bool all_ok = ZEROED || __builtin_amdgcn_ballot_w64(r.valid != kAll) == 0;
   const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const int row = cx.prow + j * Geo::ROWS_PER_LOAD;
-    const bool ok = (r.valid >> j) & 1;
-    bad_block |= !ok;
     u32x4 kp, vp;
     if constexpr (KV8) {
       kp = widen8<T>(r.k[j]);
@@ -296,8 +346,14 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<NPL, KV8>& r, const 
       kp = r.k[j];
       vp = r.v[j];
     }
-    *reinterpret_cast<u32x4*>(cx.kl + Geo::off(row, cx.pcol)) = ok ? kp : zero;
-    *reinterpret_cast<u32x4*>(cx.vl + Geo::off(row, cx.pcol)) = ok ? vp : zero;
+    if (!all_ok) {
+      const bool ok = (r.valid >> j) & 1;
+      bad_block |= !ok;
+      kp = ok ? kp : zero;
+      vp = ok ? vp : zero;
+    }
+    *reinterpret_cast<u32x4*>(cx.kl + Geo::off(row, cx.pcol)) = kp;
+    *reinterpret_cast<u32x4*>(cx.vl + Geo::off(row, cx.pcol)) = vp;
   }
 }
 
@@ -333,7 +389,7 @@ __device__ __forceinline__ void chunk_scores(const ChunkCtx& cx,
 
 // Softmax update and O^T += V^T P^T for the chunk whose scores are sacc:
 // tokens seg_lo + 32c ..., those at or past seg_hi masked out.
-template <typename T, int D, int NT>
+template <typename T, int D, int NT, bool MASK>
 __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
                                              const floatx4 (&sacc)[NT][2],
                                              WaveState<NT, D / 16>& st) {
@@ -358,7 +414,8 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int pos = cb + 16 * h + 4 * cx.grp + rr;
-        const float x = pos < cx.seg_hi ? sacc[nt][h][rr] * cx.scale_log2 : -INFINITY;
+        const float x =
+            !MASK || pos < cx.seg_hi ? sacc[nt][h][rr] * cx.scale_log2 : -INFINITY;
         sv[nt][4 * h + rr] = x;
         mx = fmaxf(mx, x);
       }
@@ -372,7 +429,7 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
       for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sv[nt][e]);
       mx = head_lanes_max(mx);
       const float m_new = fmaxf(st.m[nt], mx);
-      const float alpha = m_new == -INFINITY ? 1.f : exp2f(st.m[nt] - m_new);
+      const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(st.m[nt] - m_new);
       st.l[nt] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) st.o[nt][dt] *= alpha;
@@ -386,7 +443,7 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
     float ps = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float p = exp2f(sv[nt][e] - ref);
+      const float p = exp2_fast(sv[nt][e] - ref);
       ps += p;
       pf[nt][e] = (T)p;
     }
@@ -416,37 +473,40 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
 }
 
 // QK / softmax / PV of the chunk staged in cx's slices.
-template <typename T, int D, int NT>
+// MASK = false: the chunk lies wholly inside [seg_lo, seg_hi).
+template <typename T, int D, int NT, bool MASK = true>
 __device__ __forceinline__ void compute_chunk(int c, const ChunkCtx& cx,
                                               const typename Ops<T>::v8 (&qf)[NT][D / 32],
                                               WaveState<NT, D / 16>& st) {
   floatx4 sacc[NT][2];
   chunk_scores<T, D, NT>(cx, qf, sacc);
-  chunk_update<T, D, NT>(c, cx, sacc, st);
+  chunk_update<T, D, NT, MASK>(c, cx, sacc, st);
 }
 
 // One chunk: registers -> LDS slice, optionally refill the registers with
 // chunk `c + ahead` (issued before any compute so the loads overlap it),
 // then QK / softmax / PV out of LDS.
-template <typename T, int D, int NT, int NPL, bool OFF64, bool APP, bool KV8>
+template <typename T, int D, int NT, int NPL, bool HALVES, bool APP, bool KV8, bool MASK>
 __device__ __forceinline__ void chunk_step(
     ChunkRegs<NPL, KV8>& r, int c, bool refill, int ahead, const ChunkCtx& cx,
     const PoolView& pv, const typename Ops<T>::v8 (&qf)[NT][D / 32],
     WaveState<NT, D / 16>& st, bool& bad_block, const NewRow& nr) {
   using Geo = ChunkGeo<D>;
-  stage_chunk<T, Geo, NPL, KV8>(r, cx, bad_block);
+  stage_chunk<T, Geo, NPL, KV8, HALVES>(r, cx, bad_block);
   if constexpr (APP)
     stage_new_row<T, Geo, KV8>(nr, cx.seg_lo + c * kChunk, cx, (int)(threadIdx.x & 63));
-  if (refill) load_chunk<Geo, NPL, OFF64, KV8>(r, pv, cx, c + ahead);
-  compute_chunk<T, D, NT>(c, cx, qf, st);
+  if (refill) load_chunk<Geo, NPL, HALVES, KV8>(r, pv, cx, c + ahead);
+  compute_chunk<T, D, NT, MASK>(c, cx, qf, st);
 }
 
 // All chunks of [cx.seg_lo, cx.seg_hi) assigned to wavefront w of nw:
 // chunks w, w + nw, ... with PF chunks in flight per wavefront (APP: the
 // appended row nr is staged over its pool row where it falls). A
 // steady-state loop with no data-dependent branch keeps the compiler's wait
-// counts exact (staging buffer b waits only for buffer b's loads).
-template <typename T, int D, int NT, int PF, bool OFF64, bool APP, bool KV8>
+// counts exact (staging buffer b waits only for buffer b's loads). Only the
+// last chunk of the range can be partial, and the steady-state loop never
+// reaches it (its chunks are below nchunks - nw PF), so it skips the mask.
+template <typename T, int D, int NT, int PF, bool HALVES, bool APP, bool KV8>
 __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
                                            const PoolView& pv,
                                            const typename Ops<T>::v8 (&qf)[NT][D / 32],
@@ -459,25 +519,25 @@ __device__ __forceinline__ void run_chunks(int w, int nw, const ChunkCtx& cx,
   ChunkRegs<NPL, KV8> rb[PF];
 #pragma unroll
   for (int b = 0; b < PF; ++b)
-    if (w + nw * b < nchunks) load_chunk<Geo, NPL, OFF64, KV8>(rb[b], pv, cx, w + nw * b);
+    if (w + nw * b < nchunks) load_chunk<Geo, NPL, HALVES, KV8>(rb[b], pv, cx, w + nw * b);
   int c = w;
   for (; c + nw * (2 * PF - 1) < nchunks; c += step) {
 #pragma unroll
     for (int b = 0; b < PF; ++b)
-      chunk_step<T, D, NT, NPL, OFF64, APP, KV8>(rb[b], c + nw * b, true, step, cx, pv, qf, st,
-                                                 bad_block, nr);
+      chunk_step<T, D, NT, NPL, HALVES, APP, KV8, false>(rb[b], c + nw * b, true, step, cx, pv,
+                                                         qf, st, bad_block, nr);
   }
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
-      chunk_step<T, D, NT, NPL, OFF64, APP, KV8>(rb[b], c + nw * b, c + nw * (b + PF) < nchunks,
-                                                 step, cx, pv, qf, st, bad_block, nr);
+      chunk_step<T, D, NT, NPL, HALVES, APP, KV8, true>(
+          rb[b], c + nw * b, c + nw * (b + PF) < nchunks, step, cx, pv, qf, st, bad_block, nr);
   c += step;
 #pragma unroll
   for (int b = 0; b < PF; ++b)
     if (c + nw * b < nchunks)
-      chunk_step<T, D, NT, NPL, OFF64, APP, KV8>(rb[b], c + nw * b, false, step, cx, pv, qf, st,
-                                                 bad_block, nr);
+      chunk_step<T, D, NT, NPL, HALVES, APP, KV8, true>(rb[b], c + nw * b, false, step, cx, pv,
+                                                        qf, st, bad_block, nr);
 }
 
 // Combination of the NW wavefronts' online-softmax states of one
