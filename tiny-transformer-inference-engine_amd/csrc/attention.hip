@@ -320,8 +320,6 @@ bool sk_fits(int64_t virt, int max_blk) {
   return virt >= 1 && virt <= kMaxCounters && max_blk >= 1;
 }
 
-constexpr int64_t kPrefillWideKv = 512;
-constexpr int kPrefillWideQ = 256;
 
 AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,
@@ -354,14 +352,10 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
     return p;
   }
   if (max_q_len > 1 && max_blk >= 1 && prefill_mfma_supported(dtype, group, d)) {
-    // MFMA prefill: one workgroup per tile of query tokens, whole causal
-    // range. At 32 heads per kv head a tile is 4 tokens (two wavefronts per
-    // token) or, for query runs of kPrefillWideQ tokens and context bounds
-    // of kPrefillWideKv and more, 8 tokens (one wavefront per token with
-    // both 16-head row tiles): half the K/V re-reads across tiles, but half
-    // the workgroups and one per CU, which short runs and contexts lose.
+    // MFMA prefill: one workgroup per pair of query-token tiles (t and
+    // n - 1 - t of a sequence), whole causal range
     p.kind = 3;
-    p.rows = group == 32 && kv_bound >= kPrefillWideKv && max_q_len >= kPrefillWideQ ? 256 : 128;
+    p.rows = 128;
     p.tiles_max = 1;
     p.part_tokens = 0;
     p.parts_max = 1;

@@ -221,7 +221,6 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     a.part_tokens = plan.part_tokens;
     a.parts_max = plan.parts_max;
     a.tiles_max = plan.tiles_max;
-    a.tile_rows = plan.rows;
     float* ws = plan.ws_bytes ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                                          kWsCounterBytes)
                               : nullptr;

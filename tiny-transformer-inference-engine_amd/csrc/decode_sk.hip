@@ -98,33 +98,6 @@ __device__ __forceinline__ int share_owner(int x, int C, int W) {
 // seg_cost overhead units plus its chunks.
 __device__ __forceinline__ int sk_cost(int n, int seg_cost) { return n > 0 ? n + seg_cost : 0; }
 
-// block-wide exclusive scan of one int per thread; returns the total.
-// Each wavefront scans its 64 values with lane shuffles, then the
-// wavefront totals are combined through LDS (two barriers in all).
-__device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  int incl = x;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += y;
-  }
-  if (lane == 63) sh[w] = incl;
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) {
-    const int t = sh[i];
-    before += i < w ? t : 0;
-    total += t;
-  }
-  __syncthreads();  // sh is reused by the next scan
-  excl = before + incl - x;
-  // the same for every thread: keep it scalar
-  return __builtin_amdgcn_readfirstlane(total);
-}
-
 __device__ __forceinline__ uint64_t ld_agent64(const void* p) {
   return __hip_atomic_load(static_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -232,7 +205,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
     const ScanDesc sd = scan_desc(a, min(base + tid, V - 1), alt);
     const int n = base + tid < V ? sk_cost(sd.d.n, K) : 0;
     int ex;
-    C += block_scan(n, scan_sh, ex);
+    C += block_scan<kWaves>(n, scan_sh, ex);
     n_mine = n;
     ex_mine = ex;
     sd_mine = sd;
@@ -261,7 +234,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
       const ScanDesc sd = scan_desc(a, min(v, V - 1), alt);
       const int n = v < V ? sk_cost(sd.d.n, K) : 0;
       int ex;
-      const int tot = block_scan(n, scan_sh, ex);
+      const int tot = block_scan<kWaves>(n, scan_sh, ex);
       if (n > 0 && run + ex <= start && start < run + ex + n) {
         s_v0 = v;
         s_g0 = run + ex;

@@ -641,6 +641,34 @@ __device__ __forceinline__ void store_new_row(const char* lds, const AttnArgs& a
   }
 }
 
+// Block-wide exclusive scan of one int per thread (NW wavefronts); returns
+// the total. Each wavefront scans its 64 values with lane shuffles, then the
+// wavefront totals are combined through LDS (two barriers in all).
+template <int NW>
+__device__ __forceinline__ int block_scan(int x, int* sh, int& excl) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  int incl = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) sh[w] = incl;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int t = sh[i];
+    before += i < w ? t : 0;
+    total += t;
+  }
+  __syncthreads();  // sh is reused by the next scan
+  excl = before + incl - x;
+  // the same for every thread: keep it scalar
+  return __builtin_amdgcn_readfirstlane(total);
+}
+
 // Q^T fragments of one (token, kv head): head 16*nt + l16, dims of piece
 // 4*ks + grp.
 template <typename T, int D, int NT>

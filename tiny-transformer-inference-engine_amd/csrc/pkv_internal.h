@@ -137,7 +137,6 @@ struct AttnArgs {
   int part_tokens;   // split-K partition length (multiple of 32)
   int parts_max;     // partitions per (sequence, kv head, row tile) in grid
   int tiles_max;     // row tiles per (sequence, kv head) in grid
-  int tile_rows;     // MFMA prefill: (token, head) rows per tile, 128 or 256
   float* ws_o;       // [units][ROWS][d] unnormalised partial outputs
   float* ws_ml;      // [units][ROWS][2] (running max (log2 units), sum)
   int* status;

@@ -1,30 +1,32 @@
 // Paged MQA attention for query runs longer than one token (prefill and
-// chunked prefill) on MFMA: bf16/fp16 storage, fp32 accumulation, 16 or 32
-// query heads per KV head, head dim 64 or 128. Semantics are those of
-// pagedattn.forward (kernels/pagedattn/pagedattn.cu:142-447): query row i of
-// a sequence with q_len query tokens and kv_len keys sees keys
-// j < kv_len with, when causal, j <= kv_len - q_len + i (bottom-right
-// alignment, :196-207, :315-329); no visible key gives a zero row and
-// lse = +inf (:418-446).
+// chunked prefill) on MFMA: bf16/fp16 storage (or fp8 pools widened in
+// LDS), fp32 accumulation, 16 or 32 query heads per KV head, head dim 64 or
+// 128. Semantics are those of pagedattn.forward
+// (kernels/pagedattn/pagedattn.cu:142-447): query row i of a sequence with
+// q_len query tokens and kv_len keys sees keys j < kv_len with, when causal,
+// j <= kv_len - q_len + i (bottom-right alignment, :196-207, :315-329); no
+// visible key gives a zero row and lse = +inf (:418-446).
 //
-// A workgroup of 8 wavefronts owns a tile of query tokens of one KV head:
-// each token's G heads are covered by WPT wavefronts of NT 16-head row tiles
-// each (G = 16 NT WPT; the NT tiles of a wavefront share every K and V^T
-// fragment it reads), so a tile holds TQ = 8 / WPT tokens: 8 tokens x 16
-// heads, 4 x 32, or 8 x 32 with two row tiles per wavefront, chosen by the
-// host for long contexts (fewer K/V re-reads across tiles). The tile's keys are walked
-// in 32-token chunks staged once in LDS (double-buffered: the next chunk's
-// loads are in flight while the wavefronts compute on the current one) and
-// shared by all 8 wavefronts, so each K/V row is read once per tile for
-// TQ G rows. Per wavefront and chunk: S^T = K Q^T, online softmax with its
-// token's causal limit, O^T += V^T P^T (the decode kernels' MFMA steps).
+// Work split. A sequence's query tokens are cut into tiles of TQ tokens (a
+// tile = TQ x G rows of one KV head: 8 tokens x 16 heads or 4 x 32; each
+// wavefront owns one token's 16-head row tile). Under a causal mask tile t
+// sees about (t + 1) TQ keys, so a workgroup takes a PAIR of tiles, t and
+// n - 1 - t: every pair of a sequence then walks about the same number of
+// key chunks, and the kernel's length is set by the average tile rather
+// than the last one. Both tiles of a pair read the same keys (tile t's are a
+// prefix of tile n - 1 - t's), so each 32-key chunk is staged in LDS once
+// (double-buffered, the next chunks' loads in flight in registers while the
+// current one is computed) and used by both tiles' wavefronts: per
+// wavefront and chunk, S^T = K Q^T, online softmax with its token's causal
+// limit, O^T += V^T P^T (the decode kernels' MFMA steps), once for its
+// token of each tile that sees the chunk. Chunks wholly below a token's
+// limit skip the score mask.
 //
-// Grid: one workgroup per tile slot, 1-D. Sequence s owns the slots
-// [base_s, base_s + ceil(q_len_s / TQ)), base_s = query_start_loc[s] / TQ + s
-// (TQ tokens per tile), a non-decreasing function of s, so
-// ceil(T / TQ) + n_seq slots cover every tile and a workgroup finds its
-// sequence with one parallel pass over query_start_loc; slots past a
-// sequence's tiles, and sequences another launch owns (qfilter), exit.
+// Grid: one workgroup per pair, 1-D over the pairs of all sequences in
+// order (a block-wide scan of the per-sequence pair counts over
+// query_start_loc finds a workgroup's sequence and pair); workgroups past
+// the last pair, and sequences another launch owns (qfilter), exit. The
+// grid is sized by an upper bound, ceil(T / 2 TQ) + n_seq.
 #include "mfma_decode_common.h"
 
 namespace pkv {
@@ -35,66 +37,139 @@ using namespace mfma;
 constexpr int kPW = 8;             // wavefronts per workgroup
 constexpr int kPBlock = 64 * kPW;  // threads
 
-template <typename T, int D, int NT, int WPT, bool OFF64, bool KV8>
-__global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(AttnArgs a) {
-  using Geo = ChunkGeo<D>;
-  using v8 = typename Ops<T>::v8;
+// Pairs of TQ-token tiles of a run of q_len query tokens.
+__device__ __forceinline__ int tile_pairs(int q_len, int tq) {
+  return ((q_len + tq - 1) / tq + 1) / 2;
+}
+
+// One wavefront's token of a tile: its Q^T fragments, online-softmax state,
+// causal key limit (0: no token) and first output row.
+template <typename T, int D>
+struct TokenRows {
+  typename Ops<T>::v8 qf[1][D / 32];
+  WaveState<1, D / 16> st;
+  int lim;
+  int64_t qrow;
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void token_chunk(TokenRows<T, D>& x, int c, int lo, int hi,
+                                            ChunkCtx& cx) {
+  const int shi = min(x.lim, hi);
+  const int cb = lo + c * kChunk;
+  if (cb >= shi) return;  // uniform across the wavefront
+  cx.seg_hi = shi;
+  if (cb + kChunk <= shi)
+    compute_chunk<T, D, 1, false>(c, cx, x.qf, x.st);
+  else
+    compute_chunk<T, D, 1, true>(c, cx, x.qf, x.st);
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void token_store(TokenRows<T, D>& x, const AttnArgs& a, int lane) {
   constexpr int DT = D / 16;
+  x.st.l[0] = head_lanes_sum(x.st.l[0]);
+  if (x.qrow < 0) return;  // no token (an active one with no visible key writes zeros)
+  const int64_t row = x.qrow + (lane & 15);
+  const float L = x.st.l[0];
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  T* __restrict__ out = static_cast<T*>(a.out) + row * D + 4 * (lane >> 4);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[16 * dt + e] = (T)(x.st.o[0][dt][e] * inv);
+  if ((lane >> 4) == 0 && a.lse) a.lse[row] = L > 0.f ? (x.st.m[0] + log2f(L)) * kLn2f : INFINITY;
+}
+
+template <typename T, int D, int WPT, bool OFF64, bool KV8>
+__global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
+  using Geo = ChunkGeo<D>;
   constexpr int CPR = Geo::CPR;
-  constexpr int PIECES = kChunk * CPR;         // 16-byte pieces of one chunk of K
-  constexpr int PER = 2 * PIECES / kPBlock;    // pieces (K and V) per thread
+  constexpr int PIECES = kChunk * CPR;       // 16-byte pieces of one chunk of K
+  constexpr int PER = 2 * PIECES / kPBlock;  // pieces (K and V) per thread
   static_assert(PER >= 1 && 2 * PIECES == PER * kPBlock, "chunk must split evenly");
+  constexpr int G = 16 * WPT;
+  constexpr int TQ = kPW / WPT;
   __shared__ __attribute__((aligned(16))) char buf[2][2 * Geo::BYTES];  // [stage][K | V]
   __shared__ int tbl[kTblCap];
-  __shared__ int s_count;
+  __shared__ int scan_sh[kPW];
+  __shared__ int s_seq, s_pair, s_qb, s_ql;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
-  constexpr int G = 16 * NT * WPT;
-  constexpr int TQ = kPW / WPT;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kvh = blockIdx.y;
   const int slot = blockIdx.x;
 
-  // ---- the sequence of this slot: s = #{s : base_s <= slot} - 1
-  int cnt = 0;
-  for (int s = tid; s < a.n_seq; s += kPBlock) cnt += a.qloc[s] / TQ + s <= slot ? 1 : 0;
-  if (tid == 0) s_count = 0;
-  __syncthreads();
-  if (cnt) atomicAdd(&s_count, cnt);
-  __syncthreads();
-  const int s = __builtin_amdgcn_readfirstlane(s_count) - 1;
-  if (s < 0) return;  // only with a malformed query_start_loc (base_0 = 0 otherwise)
-  const int q_begin = ld_meta(a.qloc, s);
-  const int q_len = ld_meta(a.qloc, s + 1) - q_begin;
-  const int tile = slot - (q_begin / TQ + s);
-  if (q_len <= 0 || (a.qfilter == 2 && q_len == 1) || tile * TQ >= q_len) return;
-  if (q_begin < 0 || q_begin + q_len > a.n_tokens) {
+  // ---- this workgroup's pair: the slot-th pair of all sequences' pairs
+  if (a.n_seq <= 0) return;
+  if (tid == 0) s_seq = -1;  // published by the scan's first barrier
+  int run = 0;
+  for (int base = 0; base < a.n_seq; base += kPBlock) {
+    const int sq = base + tid;
+    int qb = 0, ql = 0;
+    if (sq < a.n_seq) {
+      qb = a.qloc[sq];
+      ql = a.qloc[sq + 1] - qb;
+    }
+    const bool skip = ql <= 0 || (a.qfilter == 2 && ql == 1);
     // malformed query_start_loc: never index q / out outside [0, T)
-    if (a.status && tid == 0) atomicOr(a.status, PKV_STATUS_BAD_QLOC);
-    return;
+    const bool bad = !skip && (qb < 0 || qb + ql > a.n_tokens);
+    if (bad && a.status && slot == 0 && kvh == 0) atomicOr(a.status, PKV_STATUS_BAD_QLOC);
+    const int np = skip || bad ? 0 : tile_pairs(ql, TQ);
+    int ex;
+    const int tot = block_scan<kPW>(np, scan_sh, ex);
+    if (np > 0 && run + ex <= slot && slot < run + ex + np) {
+      s_seq = sq;
+      s_pair = slot - run - ex;
+      s_qb = qb;
+      s_ql = ql;
+    }
+    run += tot;
+    __syncthreads();
+    if (s_seq >= 0 || run > slot) break;
   }
+  const int s = __builtin_amdgcn_readfirstlane(s_seq);
+  if (s < 0) return;  // past the last pair
+  const int pair = __builtin_amdgcn_readfirstlane(s_pair);
+  const int q_begin = __builtin_amdgcn_readfirstlane(s_qb);
+  const int q_len = __builtin_amdgcn_readfirstlane(s_ql);
+  const int ntiles = (q_len + TQ - 1) / TQ;
+  const int tA = pair;
+  const int tB = ntiles - 1 - pair;  // >= tA; == tA: one tile (the middle one)
+
+  // ---- issued together: kv_len, the first table window (entries past
+  // the sequence's blocks stay unread: max_blk >= 1 here), both tokens' Q
   int kv_len = ld_meta(a.seq_lens, s);
+  const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
+  const int spec_n = min(a.max_blk, kTblCap);
+  const int tspec = table[min(tid, spec_n - 1)];
+  const int ti = w / WPT;
+  const int h0 = (w % WPT) * 16;
+  const int iA = tA * TQ + ti;
+  const int iB = tB * TQ + ti;
+  const bool actA = iA < q_len;
+  const bool actB = tB != tA && iB < q_len;
+  const T* __restrict__ q = static_cast<const T*>(a.q);
+  TokenRows<T, D> A, B;
+  A.qrow = actA ? ((int64_t)(q_begin + iA) * a.hq + kvh * G + h0) : -1;
+  B.qrow = actB ? ((int64_t)(q_begin + iB) * a.hq + kvh * G + h0) : -1;
+  load_q<T, D, 1>(A.qf, q, (int64_t)(q_begin + min(iA, q_len - 1)) * a.hq + kvh * G + h0,
+                  lane >> 4, lane & 15);
+  load_q<T, D, 1>(B.qf, q, (int64_t)(q_begin + min(iB, q_len - 1)) * a.hq + kvh * G + h0,
+                  lane >> 4, lane & 15);
+  A.st.reset();
+  B.st.reset();
+
   const int cap = a.max_blk << a.bs_shift;
   kv_len = kv_len < cap ? kv_len : cap;
   kv_len = kv_len > 0 ? kv_len : 0;
   const int ctx = a.causal ? max(kv_len - q_len, 0) : 0;
-  const int i0 = tile * TQ;
-  const int ntok = min(TQ, q_len - i0);
-  // this wavefront's rows: NT 16-head tiles of token i
-  const int ti = w / WPT;
-  const bool active = ti < ntok;
-  const int i = i0 + (active ? ti : 0);
-  const int h0 = (w % WPT) * 16 * NT;
-  const int lim = !active ? 0 : a.causal ? min(kv_len, ctx + i + 1) : kv_len;
-  const int kv_hi = a.causal ? min(kv_len, ctx + i0 + ntok) : kv_len;  // the tile's last token's
+  A.lim = !actA ? 0 : a.causal ? min(kv_len, ctx + iA + 1) : kv_len;
+  B.lim = !actB ? 0 : a.causal ? min(kv_len, ctx + iB + 1) : kv_len;
+  // the pair's last token's limit bounds every key either tile reads
+  const int kv_hi = a.causal ? min(kv_len, ctx + min(q_len, (tB + 1) * TQ)) : kv_len;
 
-  const T* __restrict__ q = static_cast<const T*>(a.q);
-  const int64_t qrow0 = (int64_t)(q_begin + i) * a.hq + kvh * G + h0;
-  v8 qf[NT][D / 32];
-  load_q<T, D, NT>(qf, q, qrow0, lane >> 4, lane & 15);
-
-  const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
   const char* kbase = static_cast<const char*>(a.k_pool);
   const char* vbase = static_cast<const char*>(a.v_pool);
   const int64_t row_stride = (int64_t)a.hkv * D * (KV8 ? 1 : 2);
@@ -107,8 +182,6 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
   cx.grp = lane >> 4;
   cx.l16 = lane & 15;
   cx.scale_log2 = a.scale_log2;
-  WaveState<NT, DT> st;
-  st.reset();
   bool bad_block = false;
 
   // this thread's pieces of a chunk: index p of [K pieces | V pieces]
@@ -129,7 +202,11 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
     const int blk_lo = lo >> a.bs_shift;
     const int nblk = ((hi - 1) >> a.bs_shift) + 1 - blk_lo;
     __syncthreads();  // the previous window's table and chunk buffers are no longer read
-    for (int e = tid; e < nblk; e += kPBlock) tbl[e] = table[blk_lo + e];
+    if (lo == 0) {
+      if (tid < nblk) tbl[tid] = tspec;  // nblk <= spec_n: kv_hi <= max_blk blocks
+    } else {
+      for (int e = tid; e < nblk; e += kPBlock) tbl[e] = table[blk_lo + e];
+    }
     __syncthreads();
     const int nch = (hi - lo + kChunk - 1) / kChunk;
     // chunk c's pieces into registers; rows past hi re-read the window's
@@ -164,7 +241,7 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
     };
     // stage chunk c into LDS buffer c & 1 (free: every wavefront passed the
     // previous barrier after computing chunk c - 2), request chunk c + 2
-    // into the same registers, then compute chunk c
+    // into the same registers, then compute chunk c for both tokens
     auto step = [&](int c, Piece (&rg)[PER], unsigned& okm) {
       char* kl = buf[c & 1];
 #pragma unroll
@@ -184,8 +261,8 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
       cx.kl = kl;
       cx.vl = kl + Geo::BYTES;
       cx.seg_lo = lo;
-      cx.seg_hi = min(lim, hi);
-      if (lo + c * kChunk < cx.seg_hi) compute_chunk<T, D, NT>(c, cx, qf, st);
+      token_chunk<T, D>(A, c, lo, hi, cx);
+      token_chunk<T, D>(B, c, lo, hi, cx);
     };
     issue(0, rgA, okA);
     issue(1, rgB, okB);
@@ -196,41 +273,27 @@ __global__ __launch_bounds__(kPBlock, NT == 1 ? 4 : 2) void prefill_mfma_kernel(
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
 
-  // ---- finalise this wavefront's 16 NT rows
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) st.l[nt] = head_lanes_sum(st.l[nt]);
-  if (!active) return;
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int64_t row = qrow0 + 16 * nt + (lane & 15);
-    const float L = st.l[nt];
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    T* __restrict__ out = static_cast<T*>(a.out) + row * D + 4 * (lane >> 4);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) out[16 * dt + e] = (T)(st.o[nt][dt][e] * inv);
-    if ((lane >> 4) == 0 && a.lse)
-      a.lse[row] = L > 0.f ? (st.m[nt] + log2f(L)) * kLn2f : INFINITY;
-  }
+  // ---- finalise the wavefront's 16 rows of each token
+  token_store<T, D>(A, a, lane);
+  token_store<T, D>(B, a, lane);
 }
 
-template <typename T, int NT, int WPT, bool OFF64>
-int launch_nt(const AttnArgs& a, hipStream_t stream) {
+template <typename T, int WPT, bool OFF64>
+int launch_wpt(const AttnArgs& a, hipStream_t stream) {
   constexpr int tq = kPW / WPT;
-  const dim3 grid((a.n_tokens + tq - 1) / tq + a.n_seq, a.hkv);
+  const dim3 grid((a.n_tokens + 2 * tq - 1) / (2 * tq) + a.n_seq, a.hkv);
   if (a.d == 64 && a.kv8)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, NT, WPT, OFF64, true>), grid, dim3(kPBlock),
-                       0, stream, a);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, WPT, OFF64, true>), grid, dim3(kPBlock), 0,
+                       stream, a);
   else if (a.d == 64)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, NT, WPT, OFF64, false>), grid, dim3(kPBlock),
-                       0, stream, a);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 64, WPT, OFF64, false>), grid, dim3(kPBlock), 0,
+                       stream, a);
   else if (a.d == 128 && a.kv8)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, NT, WPT, OFF64, true>), grid, dim3(kPBlock),
-                       0, stream, a);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, WPT, OFF64, true>), grid, dim3(kPBlock), 0,
+                       stream, a);
   else if (a.d == 128)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, NT, WPT, OFF64, false>), grid,
-                       dim3(kPBlock), 0, stream, a);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, WPT, OFF64, false>), grid, dim3(kPBlock), 0,
+                       stream, a);
   else
     return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: d=%d", a.d);
   return check_launch("prefill_mfma_kernel");
@@ -238,9 +301,8 @@ int launch_nt(const AttnArgs& a, hipStream_t stream) {
 
 template <typename T, bool OFF64>
 int launch_t(const AttnArgs& a, hipStream_t stream) {
-  if (a.group == 16) return launch_nt<T, 1, 1, OFF64>(a, stream);
-  if (a.group == 32 && a.tile_rows == 256) return launch_nt<T, 2, 1, OFF64>(a, stream);
-  if (a.group == 32) return launch_nt<T, 1, 2, OFF64>(a, stream);
+  if (a.group == 16) return launch_wpt<T, 1, OFF64>(a, stream);
+  if (a.group == 32) return launch_wpt<T, 2, OFF64>(a, stream);
   return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: %d query heads per kv head", a.group);
 }
 
@@ -253,10 +315,11 @@ bool prefill_mfma_supported(int dtype, int group, int d) {
 
 int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t stream) {
   if (!a.qloc) return fail(PKV_ERR_INVALID, "prefill_mfma: query_start_loc required");
-  const int tq = a.group == 32 && a.tile_rows != 256 ? kPW / 2 : kPW;
-  const int64_t slots = ((int64_t)a.n_tokens + tq - 1) / tq + a.n_seq;
+  if (a.max_blk < 1) return fail(PKV_ERR_INVALID, "prefill_mfma: empty block table");
+  const int tq = a.group == 32 ? kPW / 2 : kPW;
+  const int64_t slots = ((int64_t)a.n_tokens + 2 * tq - 1) / (2 * tq) + a.n_seq;
   if (slots > 0x7fffffff)
-    return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: %lld tile slots", (long long)slots);
+    return fail(PKV_ERR_UNSUPPORTED, "prefill_mfma: %lld tile pairs", (long long)slots);
   const bool off64 = pool_needs_off64(a);
   if (dtype == PKV_DTYPE_BF16)
     return off64 ? launch_t<bf16, true>(a, stream) : launch_t<bf16, false>(a, stream);
