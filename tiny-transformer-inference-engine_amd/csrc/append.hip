@@ -77,6 +77,11 @@ __device__ __forceinline__ int seq_of_token(const int32_t* __restrict__ qloc,
   return lo;
 }
 
+// query_start_loc entries a workgroup of the table append stages in LDS
+// (one coalesced read instead of a chain of dependent global reads per
+// binary-search step); longer batches search the global array.
+constexpr int kQlocLds = 4096;
+
 template <int VEC>
 __global__ __launch_bounds__(kThreads) void append_table_kernel(
     char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t num_blocks,
@@ -86,20 +91,27 @@ __global__ __launch_bounds__(kThreads) void append_table_kernel(
     const int32_t* __restrict__ start_pos, int n_seq, int64_t n_tok,
     int64_t row_bytes, int min_qlen, int* status) {
   using V = typename VecT<VEC>::type;
+  __shared__ int32_t qs[kQlocLds];
   const int64_t ppr = row_bytes / VEC;
   const int64_t total = n_tok * ppr;
   const char* __restrict__ src = blockIdx.y ? v_new : k_new;
   char* __restrict__ dst = blockIdx.y ? v_pool : k_pool;
   const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const bool in_lds = n_seq + 1 <= kQlocLds;
+  if (in_lds) {
+    for (int i = threadIdx.x; i <= n_seq; i += kThreads) qs[i] = qloc[i];
+    __syncthreads();
+  }
+  const int32_t* ql = in_lds ? qs : qloc;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
        i += stride) {
     const int64_t tok = i / ppr;
     const int64_t pc = i - tok * ppr;
-    const int s = seq_of_token(qloc, n_seq, tok);
+    const int s = seq_of_token(ql, n_seq, tok);
     // rows of sequences with fewer than min_qlen tokens are another
     // launch's (the fused decode append of a mixed batch)
-    if (min_qlen > 1 && qloc[s + 1] - qloc[s] < min_qlen) continue;
-    const int64_t pos = (int64_t)start_pos[s] + (tok - qloc[s]);
+    if (min_qlen > 1 && ql[s + 1] - ql[s] < min_qlen) continue;
+    const int64_t pos = (int64_t)start_pos[s] + (tok - ql[s]);
     const int64_t page = pos >> bs_shift;
     const bool flag = status && pc == 0 && blockIdx.y == 0;
     if (pos < 0 || page >= max_blk) {
@@ -198,17 +210,24 @@ __global__ __launch_bounds__(kThreads) void append_table_fp8_kernel(
     const int32_t* __restrict__ tables, int max_blk, const int32_t* __restrict__ qloc,
     const int32_t* __restrict__ start_pos, int n_seq, int64_t n_tok, int64_t row_elems,
     int min_qlen, int* status) {
+  __shared__ int32_t qs[kQlocLds];
   const int64_t ppr = row_elems / 8;
   const int64_t total = n_tok * ppr;
   const S* __restrict__ src = blockIdx.y ? v_new : k_new;
   char* __restrict__ dst = blockIdx.y ? v_pool : k_pool;
   const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const bool in_lds = n_seq + 1 <= kQlocLds;
+  if (in_lds) {
+    for (int i = threadIdx.x; i <= n_seq; i += kThreads) qs[i] = qloc[i];
+    __syncthreads();
+  }
+  const int32_t* ql = in_lds ? qs : qloc;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += stride) {
     const int64_t tok = i / ppr;
     const int64_t pc = i - tok * ppr;
-    const int s = seq_of_token(qloc, n_seq, tok);
-    if (min_qlen > 1 && qloc[s + 1] - qloc[s] < min_qlen) continue;
-    const int64_t pos = (int64_t)start_pos[s] + (tok - qloc[s]);
+    const int s = seq_of_token(ql, n_seq, tok);
+    if (min_qlen > 1 && ql[s + 1] - ql[s] < min_qlen) continue;
+    const int64_t pos = (int64_t)start_pos[s] + (tok - ql[s]);
     const int64_t page = pos >> bs_shift;
     const bool flag = status && pc == 0 && blockIdx.y == 0;
     if (pos < 0 || page >= max_blk) {
