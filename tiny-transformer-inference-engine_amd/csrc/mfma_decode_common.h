@@ -404,6 +404,8 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
   // relative terms, and most chunks skip the shuffles and the rescale.
   // P^T operand = this lane's 8 probabilities.
   const int cb = cx.seg_lo + c * kChunk;
+  // token 16h + 4 grp + rr of the chunk is in range iff 16h + rr < lim
+  const int lim = cx.seg_hi - cb - 4 * cx.grp;
   float sv[NT][8];
   bool move = false;
 #pragma unroll
@@ -413,9 +415,8 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const int pos = cb + 16 * h + 4 * cx.grp + rr;
         const float x =
-            !MASK || pos < cx.seg_hi ? sacc[nt][h][rr] * cx.scale_log2 : -INFINITY;
+            !MASK || 16 * h + rr < lim ? sacc[nt][h][rr] * cx.scale_log2 : -INFINITY;
         sv[nt][4 * h + rr] = x;
         mx = fmaxf(mx, x);
       }

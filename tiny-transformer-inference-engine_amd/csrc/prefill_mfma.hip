@@ -59,10 +59,7 @@ __device__ __forceinline__ void token_chunk(TokenRows<T, D>& x, int c, int lo, i
   const int cb = lo + c * kChunk;
   if (cb >= shi) return;  // uniform across the wavefront
   cx.seg_hi = shi;
-  if (cb + kChunk <= shi)
-    compute_chunk<T, D, 1, false>(c, cx, x.qf, x.st);
-  else
-    compute_chunk<T, D, 1, true>(c, cx, x.qf, x.st);
+  compute_chunk<T, D, 1, true>(c, cx, x.qf, x.st);
 }
 
 template <typename T, int D>
