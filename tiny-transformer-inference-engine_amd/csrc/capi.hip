@@ -242,30 +242,45 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
         v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens, row_bytes,
         min_qlen, status, (hipStream_t)stream);
   };
-  // Only the split-K partition decode kernel takes the append fused: for
-  // the persistent kernel the fused form measured slower than a separate
-  // append launch (register pressure at 32 heads x 128 dims), and the
-  // prefill and generic kernels read every row from the pool.
+  // The split-K partition decode kernel and the MFMA prefill kernel (16-bit
+  // pools) take the append fused: the partition kernel the one row of each
+  // sequence, the prefill kernel every row of the batch (each workgroup a
+  // share of the rows; its attention takes its own sequences' new rows from
+  // k_new / v_new). For the persistent decode kernel the fused form measured
+  // slower than a separate append launch (register pressure at 32 heads x
+  // 128 dims), and the generic kernel reads every row from the pool.
+  const bool fuse_pre = k_new && !kv8 && n_seq <= kPrefillFuseMaxSeq;
   if (!sp.mixed) {
     AttnArgs a = args_for(sp.dec, 0);
     if (k_new) {
-      if (sp.dec.kind != 1) {
-        // append, then attend
-        const int rc = append_rows(0);
-        if (rc != PKV_OK) return rc;
-      } else {
+      if (sp.dec.kind == 1 || (sp.dec.kind == 3 && fuse_pre)) {
         a.k_new = k_new;
         a.v_new = v_new;
         a.new_pos = start_pos;
+      } else {
+        // append, then attend
+        const int rc = append_rows(0);
+        if (rc != PKV_OK) return rc;
       }
     }
     return launch_attention(a, sp.dec, qdtype, (hipStream_t)stream);
   }
-  // mixed batch: the decode sequences on an MFMA decode kernel, then the
-  // prefill sequences; the prefill rows (and the decode rows unless the
-  // decode kernel takes them fused) are appended first
+  // mixed batch: the decode sequences on an MFMA decode kernel, the
+  // prefill sequences on the prefill kernel. With the fused append the
+  // prefill kernel runs first and appends every row (the decode kernel
+  // after it reads them from the pool); otherwise the prefill rows (and the
+  // decode rows unless the decode kernel takes them fused) are appended
+  // first and the decode kernel runs first.
   AttnArgs ad = args_for(sp.dec, 1);
-  const AttnArgs ap = args_for(sp.pre, 2);
+  AttnArgs ap = args_for(sp.pre, 2);
+  if (fuse_pre && sp.pre.kind == 3) {
+    ap.k_new = k_new;
+    ap.v_new = v_new;
+    ap.new_pos = start_pos;
+    const int rc = launch_attention(ap, sp.pre, qdtype, (hipStream_t)stream);
+    if (rc != PKV_OK) return rc;
+    return launch_attention(ad, sp.dec, qdtype, (hipStream_t)stream);
+  }
   if (k_new) {
     const bool fuse = sp.dec.kind == 1;
     const int rc = append_rows(fuse ? 2 : 0);

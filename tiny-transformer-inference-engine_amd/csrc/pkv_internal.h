@@ -140,9 +140,10 @@ struct AttnArgs {
   float* ws_o;       // [units][ROWS][d] unnormalised partial outputs
   float* ws_ml;      // [units][ROWS][2] (running max (log2 units), sum)
   int* status;
-  // fused append (decode MFMA kernels; all null otherwise): the K/V row of
-  // sequence s's query token goes to position new_pos[s] of its table, and
-  // the attention uses it from k_new / v_new
+  // fused append (partition decode kernel and MFMA prefill kernel; all null
+  // otherwise): the K/V rows of sequence s's query tokens go to positions
+  // new_pos[s], new_pos[s] + 1, ... of its table, and the attention uses
+  // them from k_new / v_new
   const void* k_new;
   const void* v_new;
   const int32_t* new_pos;
@@ -156,6 +157,9 @@ struct AttnArgs {
 // Rows ((query token, head) pairs of one kv head) per tile of the generic
 // kernel.
 constexpr int kGenRows = 32;
+// The MFMA prefill kernel takes the append fused for batches of at most
+// this many sequences (one block of its query_start_loc scan).
+constexpr int kPrefillFuseMaxSeq = 512;
 constexpr int kChunk = 32;  // kv tokens staged per iteration
 
 // Workspace layout: the first kWsCounterBytes are a header. Its first

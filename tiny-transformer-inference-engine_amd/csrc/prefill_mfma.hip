@@ -36,6 +36,7 @@ using namespace mfma;
 
 constexpr int kPW = 8;             // wavefronts per workgroup
 constexpr int kPBlock = 64 * kPW;  // threads
+static_assert(kPBlock == kPrefillFuseMaxSeq, "the fused append's scan is one block");
 
 // Pairs of TQ-token tiles of a run of q_len query tokens.
 __device__ __forceinline__ int tile_pairs(int q_len, int tq) {
@@ -78,6 +79,40 @@ __device__ __forceinline__ void token_store(TokenRows<T, D>& x, const AttnArgs& 
   if ((lane >> 4) == 0 && a.lse) a.lse[row] = L > 0.f ? (x.st.m[0] + log2f(L)) * kLn2f : INFINITY;
 }
 
+// One piece of the fused append: 16 bytes of the K or V row (kv head kvh)
+// of token tok, at position pos of sequence s, written with the checks of
+// the stand-alone table append (pagedkv append_from_table): a position past
+// the table raises SHORT_TABLE, an entry outside [1, blocks) raises
+// BAD_BLOCK, and neither writes. phys < 0: read the entry from the table.
+template <int D>
+__device__ __forceinline__ void append_store(const AttnArgs& a, int s, int pos, int64_t phys,
+                                             int kvh, int pc, u32x4 v) {
+  constexpr int PPR = D * 2 / 16;  // pieces per K (or V) row
+  const int page = pos >> a.bs_shift;
+  const bool flag = a.status && pc == 0 && kvh == 0;
+  if (pos < 0 || page >= a.max_blk) {
+    if (flag) atomicOr(a.status, PKV_STATUS_SHORT_TABLE);
+    return;
+  }
+  if (phys < 0) phys = a.block_tables[(int64_t)s * a.max_blk + page];
+  if (phys <= 0 || phys >= a.num_blocks) {
+    if (flag) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
+    return;
+  }
+  const bool is_v = pc >= PPR;
+  const int64_t slot = (phys << a.bs_shift) + (pos & ((1 << a.bs_shift) - 1));
+  char* pool = static_cast<char*>(const_cast<void*>(is_v ? a.v_pool : a.k_pool));
+  *reinterpret_cast<u32x4*>(pool + (slot * a.hkv + kvh) * D * 2 + (pc % PPR) * 16) = v;
+}
+
+template <int D>
+__device__ __forceinline__ u32x4 new_piece(const AttnArgs& a, int tok, int kvh, int pc) {
+  constexpr int PPR = D * 2 / 16;
+  const char* src = static_cast<const char*>(pc >= PPR ? a.v_new : a.k_new);
+  return *reinterpret_cast<const u32x4*>(src + ((int64_t)tok * a.hkv + kvh) * D * 2 +
+                                         (pc % PPR) * 16);
+}
+
 template <typename T, int D, int WPT, bool OFF64, bool KV8>
 __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
   using Geo = ChunkGeo<D>;
@@ -91,6 +126,7 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
   __shared__ int tbl[kTblCap];
   __shared__ int scan_sh[kPW];
   __shared__ int s_seq, s_pair, s_qb, s_ql;
+  __shared__ int dl_seq[kPBlock], dl_tok[kPBlock];  // fused append: this pair's decode rows
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -98,10 +134,17 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
   const int kvh = blockIdx.y;
   const int slot = blockIdx.x;
 
-  // ---- this workgroup's pair: the slot-th pair of all sequences' pairs
+  // ---- this workgroup's pair: the slot-th pair of all sequences' pairs.
+  // With the fused append (at most kPBlock sequences: one scan block) the
+  // scan also numbers the one-token sequences this launch does not attend
+  // (a mixed batch's decode rows): pair workgroup p of P appends decode rows
+  // [p ND / P, (p + 1) ND / P), and every pair workgroup its own tokens' rows.
   if (a.n_seq <= 0) return;
+  const bool fused = a.k_new != nullptr;
+  constexpr int PPR = D * 2 / 16;  // 16-byte pieces per K (or V) row
   if (tid == 0) s_seq = -1;  // published by the scan's first barrier
-  int run = 0;
+  int run = 0, run_d = 0;
+  int my_dex = -1, my_sq = 0, my_tok = 0;  // fused: this thread's decode row
   for (int base = 0; base < a.n_seq; base += kPBlock) {
     const int sq = base + tid;
     int qb = 0, ql = 0;
@@ -116,6 +159,17 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
     const int np = skip || bad ? 0 : tile_pairs(ql, TQ);
     int ex;
     const int tot = block_scan<kPW>(np, scan_sh, ex);
+    if (fused) {
+      const int nd = ql == 1 && skip && qb >= 0 && qb < a.n_tokens ? 1 : 0;
+      int exd;
+      const int totd = block_scan<kPW>(nd, scan_sh, exd);
+      if (nd) {
+        my_dex = run_d + exd;
+        my_sq = sq;
+        my_tok = qb;
+      }
+      run_d += totd;
+    }
     if (np > 0 && run + ex <= slot && slot < run + ex + np) {
       s_seq = sq;
       s_pair = slot - run - ex;
@@ -124,10 +178,19 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
     }
     run += tot;
     __syncthreads();
-    if (s_seq >= 0 || run > slot) break;
+    if (!fused && (s_seq >= 0 || run > slot)) break;
   }
   const int s = __builtin_amdgcn_readfirstlane(s_seq);
   if (s < 0) return;  // past the last pair
+  // fused: this pair's decode rows, listed in LDS (published by the first
+  // table window's barrier)
+  const int P = run;
+  const int dj0 = (int)((int64_t)slot * run_d / P);
+  const int nd_rows = (int)((int64_t)(slot + 1) * run_d / P) - dj0;
+  if (fused && my_dex >= dj0 && my_dex < dj0 + nd_rows) {
+    dl_seq[my_dex - dj0] = my_sq;
+    dl_tok[my_dex - dj0] = my_tok;
+  }
   const int pair = __builtin_amdgcn_readfirstlane(s_pair);
   const int q_begin = __builtin_amdgcn_readfirstlane(s_qb);
   const int q_len = __builtin_amdgcn_readfirstlane(s_ql);
@@ -138,6 +201,25 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
   // ---- issued together: kv_len, the first table window (entries past
   // the sequence's blocks stay unread: max_blk >= 1 here), both tokens' Q
   int kv_len = ld_meta(a.seq_lens, s);
+  // fused: positions [sp, sp + q_len) are this sequence's new rows, read
+  // from k_new / v_new (row q_begin + pos - sp) instead of the pool
+  const int sp = fused ? ld_meta(a.new_pos, s) : 0;
+  // fused: the rows of this pair's own tokens (tile A's, then tile B's),
+  // one piece per thread, requested now and written once the first table
+  // window is in LDS
+  const int nA = min(TQ, q_len - tA * TQ);
+  const int n_own = nA + (tB != tA ? min(TQ, q_len - tB * TQ) : 0);
+  const int own_u = tid / (2 * PPR);
+  const int own_i = own_u < nA ? tA * TQ + own_u : tB * TQ + (own_u - nA);
+  const bool own = fused && own_u < n_own;
+  u32x4 own_v{};
+  if (own) own_v = new_piece<D>(a, q_begin + own_i, kvh, tid % (2 * PPR));
+  // fused: this thread's piece of the pair's first kPBlock decode-row
+  // pieces, requested once the list is in LDS (the rest at the end)
+  const bool dec = fused && tid < nd_rows * 2 * PPR;
+  int d_sq = 0, d_pos = -1;
+  int64_t d_phys = -1;
+  u32x4 d_v{};
   const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
   const int spec_n = min(a.max_blk, kTblCap);
   const int tspec = table[min(tid, spec_n - 1)];
@@ -205,6 +287,17 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
       for (int e = tid; e < nblk; e += kPBlock) tbl[e] = table[blk_lo + e];
     }
     __syncthreads();
+    if (lo == 0 && own) {
+      const int pos = sp + own_i;
+      const int page = pos >> a.bs_shift;
+      append_store<D>(a, s, pos, page >= 0 && page < nblk ? tbl[page] : -1, kvh,
+                      tid % (2 * PPR), own_v);
+    }
+    if (lo == 0 && dec) {  // the decode list is published: request row and position
+      d_sq = dl_seq[tid / (2 * PPR)];
+      d_pos = a.new_pos[d_sq];
+      d_v = new_piece<D>(a, dl_tok[tid / (2 * PPR)], kvh, tid % (2 * PPR));
+    }
     const int nch = (hi - lo + kChunk - 1) / kChunk;
     // chunk c's pieces into registers; rows past hi re-read the window's
     // last row (masked), rows whose table entry is outside the pool read
@@ -226,14 +319,17 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
         okm |= (unsigned)ok << k;
         const int slotv = ((ok ? phys : 0) << a.bs_shift) + (pos & bs_mask);
         const char* base = is_v(k) ? vbase : kbase;
-        if constexpr (OFF64) {
-          rg[k] = *reinterpret_cast<const Piece*>(base + (int64_t)slotv * row_stride + head_off +
-                                                  pcol[k] * PB);
-        } else {
-          rg[k] = *reinterpret_cast<const Piece*>(
-              base + ((unsigned)slotv * (unsigned)row_stride + (unsigned)head_off +
-                      (unsigned)(pcol[k] * PB)));
+        const char* src;
+        if constexpr (OFF64)
+          src = base + (int64_t)slotv * row_stride + head_off + pcol[k] * PB;
+        else
+          src = base + ((unsigned)slotv * (unsigned)row_stride + (unsigned)head_off +
+                        (unsigned)(pcol[k] * PB));
+        if (!KV8 && fused && pos >= sp && pos < sp + q_len) {
+          const char* nb = static_cast<const char*>(is_v(k) ? a.v_new : a.k_new);
+          src = nb + ((int64_t)(q_begin + pos - sp) * a.hkv + kvh) * D * 2 + pcol[k] * PB;
         }
+        rg[k] = *reinterpret_cast<const Piece*>(src);
       }
     };
     // stage chunk c into LDS buffer c & 1 (free: every wavefront passed the
@@ -260,6 +356,11 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
       cx.seg_lo = lo;
       token_chunk<T, D>(A, c, lo, hi, cx);
       token_chunk<T, D>(B, c, lo, hi, cx);
+      if (lo == 0 && c == 0 && dec) {  // its position has arrived: request the table entry
+        const int page = d_pos >> a.bs_shift;
+        if (d_pos >= 0 && page < a.max_blk)
+          d_phys = a.block_tables[(int64_t)d_sq * a.max_blk + page];
+      }
     };
     issue(0, rgA, okA);
     issue(1, rgB, okB);
@@ -273,6 +374,23 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
   // ---- finalise the wavefront's 16 rows of each token
   token_store<T, D>(A, a, lane);
   token_store<T, D>(B, a, lane);
+  if (fused) {
+    if (kv_hi <= 0) {  // no window ran: publish the decode list, request now
+      __syncthreads();
+      if (dec) {
+        d_sq = dl_seq[tid / (2 * PPR)];
+        d_pos = a.new_pos[d_sq];
+        d_v = new_piece<D>(a, dl_tok[tid / (2 * PPR)], kvh, tid % (2 * PPR));
+      }
+    }
+    if (dec) append_store<D>(a, d_sq, d_pos, d_phys, kvh, tid % (2 * PPR), d_v);
+    for (int i = tid + kPBlock; i < nd_rows * 2 * PPR; i += kPBlock) {
+      const int r = i / (2 * PPR);
+      const int sq = dl_seq[r];
+      append_store<D>(a, sq, a.new_pos[sq], -1, kvh, i % (2 * PPR),
+                      new_piece<D>(a, dl_tok[r], kvh, i % (2 * PPR)));
+    }
+  }
 }
 
 template <typename T, int WPT, bool OFF64>
