@@ -358,21 +358,23 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<NPL, KV8>& r, const 
 }
 
 // S^T = K Q^T of the chunk staged in cx's K slice: tokens 16h + 4*grp + r
-// of the chunk for head 16nt + l16.
-template <typename T, int D, int NT>
-__device__ __forceinline__ void chunk_scores(const ChunkCtx& cx,
-                                             const typename Ops<T>::v8 (&qf)[NT][D / 32],
-                                             floatx4 (&sacc)[NT][2]) {
+// of the chunk for head 16nt + l16, for the NC row tiles N0 ... of qf (each
+// K fragment is read once for all of them).
+template <typename T, int D, int NT, int N0, int NC>
+__device__ __forceinline__ void chunk_scores_sub(const ChunkCtx& cx,
+                                                 const typename Ops<T>::v8 (&qf)[NT][D / 32],
+                                                 floatx4 (&sacc)[NC][2]) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
   constexpr int KS = D / 32;
+  static_assert(N0 >= 0 && NC >= 1 && N0 + NC <= NT, "row tiles");
   // the slice is private to this wavefront: waiting for its own LDS writes
   // is the only synchronisation the reads below need
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   // k-step outermost: one K fragment live at a time (each accumulator still
   // sums its k-steps in order 0, 1, ...)
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
+  for (int nt = 0; nt < NC; ++nt)
 #pragma unroll
     for (int h = 0; h < 2; ++h) sacc[nt][h] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -382,17 +384,27 @@ __device__ __forceinline__ void chunk_scores(const ChunkCtx& cx,
       const v8 kf =
           *reinterpret_cast<const v8*>(cx.kl + Geo::off(16 * h + cx.l16, 4 * ks + cx.grp));
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) sacc[nt][h] = Ops<T>::mma(kf, qf[nt][ks], sacc[nt][h]);
+      for (int nt = 0; nt < NC; ++nt)
+        sacc[nt][h] = Ops<T>::mma(kf, qf[N0 + nt][ks], sacc[nt][h]);
     }
   }
 }
+template <typename T, int D, int NT>
+__device__ __forceinline__ void chunk_scores(const ChunkCtx& cx,
+                                             const typename Ops<T>::v8 (&qf)[NT][D / 32],
+                                             floatx4 (&sacc)[NT][2]) {
+  chunk_scores_sub<T, D, NT, 0, NT>(cx, qf, sacc);
+}
 
-// Softmax update and O^T += V^T P^T for the chunk whose scores are sacc:
-// tokens seg_lo + 32c ..., those at or past seg_hi masked out.
-template <typename T, int D, int NT, bool MASK>
-__device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
-                                             const floatx4 (&sacc)[NT][2],
-                                             WaveState<NT, D / 16>& st) {
+// Softmax update and O^T += V^T P^T for the chunk whose scores are sacc
+// (row tiles N0 ... N0 + NC - 1 of st): tokens seg_lo + 32c ..., those at or
+// past seg_hi[nt] masked out for row tile N0 + nt (each V^T fragment is
+// read once for all of them).
+template <typename T, int D, int NT, int N0, int NC, bool MASK>
+__device__ __forceinline__ void chunk_update_sub(int c, const ChunkCtx& cx,
+                                                 const int (&seg_hi)[NC],
+                                                 const floatx4 (&sacc)[NC][2],
+                                                 WaveState<NT, D / 16>& st) {
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
   constexpr int DT = D / 16;
@@ -404,12 +416,12 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
   // relative terms, and most chunks skip the shuffles and the rescale.
   // P^T operand = this lane's 8 probabilities.
   const int cb = cx.seg_lo + c * kChunk;
-  // token 16h + 4 grp + rr of the chunk is in range iff 16h + rr < lim
-  const int lim = cx.seg_hi - cb - 4 * cx.grp;
-  float sv[NT][8];
+  float sv[NC][8];
   bool move = false;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < NC; ++nt) {
+    // token 16h + 4 grp + rr of the chunk is in range iff 16h + rr < lim
+    const int lim = seg_hi[nt] - cb - 4 * cx.grp;
     float mx = -INFINITY;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -420,27 +432,27 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
         sv[nt][4 * h + rr] = x;
         mx = fmaxf(mx, x);
       }
-    move |= mx > st.m[nt] + kLazy;  // also true on the first scores (m = -inf)
+    move |= mx > st.m[N0 + nt] + kLazy;  // also true on the first scores (m = -inf)
   }
   if (__builtin_amdgcn_ballot_w64(move) != 0) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int nt = 0; nt < NC; ++nt) {
       float mx = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sv[nt][e]);
       mx = head_lanes_max(mx);
-      const float m_new = fmaxf(st.m[nt], mx);
-      const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(st.m[nt] - m_new);
-      st.l[nt] *= alpha;
+      const float m_new = fmaxf(st.m[N0 + nt], mx);
+      const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(st.m[N0 + nt] - m_new);
+      st.l[N0 + nt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) st.o[nt][dt] *= alpha;
-      st.m[nt] = m_new;
+      for (int dt = 0; dt < DT; ++dt) st.o[N0 + nt][dt] *= alpha;
+      st.m[N0 + nt] = m_new;
     }
   }
-  v8 pf[NT];
+  v8 pf[NC];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const float ref = st.m[nt] == -INFINITY ? 0.f : st.m[nt];
+  for (int nt = 0; nt < NC; ++nt) {
+    const float ref = st.m[N0 + nt] == -INFINITY ? 0.f : st.m[N0 + nt];
     float ps = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -448,7 +460,7 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
       ps += p;
       pf[nt][e] = (T)p;
     }
-    st.l[nt] += ps;
+    st.l[N0 + nt] += ps;
   }
 
   // O^T += V^T P^T; V^T fragment: dims 16dt + l16, the same 8 tokens
@@ -469,8 +481,18 @@ __device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
     v8 vf;
     __builtin_memcpy(&vf, &both, 16);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) st.o[nt][dt] = Ops<T>::mma(vf, pf[nt], st.o[nt][dt]);
+    for (int nt = 0; nt < NC; ++nt)
+      st.o[N0 + nt][dt] = Ops<T>::mma(vf, pf[nt], st.o[N0 + nt][dt]);
   }
+}
+template <typename T, int D, int NT, bool MASK>
+__device__ __forceinline__ void chunk_update(int c, const ChunkCtx& cx,
+                                             const floatx4 (&sacc)[NT][2],
+                                             WaveState<NT, D / 16>& st) {
+  int seg_hi[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) seg_hi[nt] = cx.seg_hi;
+  chunk_update_sub<T, D, NT, 0, NT, MASK>(c, cx, seg_hi, sacc, st);
 }
 
 // QK / softmax / PV of the chunk staged in cx's slices.

@@ -29,6 +29,8 @@
 // grid is sized by an upper bound, ceil(T / 2 TQ) + n_seq.
 #include "mfma_decode_common.h"
 
+#include <type_traits>
+
 namespace pkv {
 namespace {
 
@@ -43,40 +45,55 @@ __device__ __forceinline__ int tile_pairs(int q_len, int tq) {
   return ((q_len + tq - 1) / tq + 1) / 2;
 }
 
-// One wavefront's token of a tile: its Q^T fragments, online-softmax state,
-// causal key limit (0: no token) and first output row.
+// A wavefront's two tokens (tile t's and tile n-1-t's), each one 16-head
+// row tile: Q^T fragments and online-softmax state as row tiles 0 (token A)
+// and 1 (token B), causal key limits (0: no token) and first output rows
+// (-1: no token).
 template <typename T, int D>
-struct TokenRows {
-  typename Ops<T>::v8 qf[1][D / 32];
-  WaveState<1, D / 16> st;
-  int lim;
-  int64_t qrow;
+struct PairRows {
+  typename Ops<T>::v8 qf[2][D / 32];
+  WaveState<2, D / 16> st;
+  int lim[2];
+  int64_t qrow[2];
 };
 
-template <typename T, int D>
-__device__ __forceinline__ void token_chunk(TokenRows<T, D>& x, int c, int lo, int hi,
-                                            ChunkCtx& cx) {
-  const int shi = min(x.lim, hi);
-  const int cb = lo + c * kChunk;
-  if (cb >= shi) return;  // uniform across the wavefront
-  cx.seg_hi = shi;
-  compute_chunk<T, D, 1, true>(c, cx, x.qf, x.st);
+// Chunk c of the window [lo, hi): BOTH, for both tokens at once (one read
+// of each K and V^T fragment for the two; the chunk lies below A's limit),
+// else for token B when it sees the chunk.
+template <typename T, int D, bool BOTH>
+__device__ __forceinline__ void pair_chunk(PairRows<T, D>& x, int c, int lo, int hi,
+                                           const ChunkCtx& cx) {
+  const int sb = min(x.lim[1], hi);
+  if constexpr (BOTH) {
+    floatx4 sacc[2][2];
+    const int sh[2] = {min(x.lim[0], hi), sb};
+    chunk_scores_sub<T, D, 2, 0, 2>(cx, x.qf, sacc);
+    chunk_update_sub<T, D, 2, 0, 2, true>(c, cx, sh, sacc, x.st);
+  } else {
+    if (lo + c * kChunk >= sb) return;  // uniform across the wavefront
+    floatx4 sacc[1][2];
+    const int sh[1] = {sb};
+    chunk_scores_sub<T, D, 2, 1, 1>(cx, x.qf, sacc);
+    chunk_update_sub<T, D, 2, 1, 1, true>(c, cx, sh, sacc, x.st);
+  }
 }
 
+// Row tile k's 16 output rows (and lse) of a wavefront.
 template <typename T, int D>
-__device__ __forceinline__ void token_store(TokenRows<T, D>& x, const AttnArgs& a, int lane) {
+__device__ __forceinline__ void pair_store(PairRows<T, D>& x, int k, const AttnArgs& a,
+                                           int lane) {
   constexpr int DT = D / 16;
-  x.st.l[0] = head_lanes_sum(x.st.l[0]);
-  if (x.qrow < 0) return;  // no token (an active one with no visible key writes zeros)
-  const int64_t row = x.qrow + (lane & 15);
-  const float L = x.st.l[0];
+  x.st.l[k] = head_lanes_sum(x.st.l[k]);
+  if (x.qrow[k] < 0) return;  // no token (an active one with no visible key writes zeros)
+  const int64_t row = x.qrow[k] + (lane & 15);
+  const float L = x.st.l[k];
   const float inv = L > 0.f ? 1.f / L : 0.f;
   T* __restrict__ out = static_cast<T*>(a.out) + row * D + 4 * (lane >> 4);
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) out[16 * dt + e] = (T)(x.st.o[0][dt][e] * inv);
-  if ((lane >> 4) == 0 && a.lse) a.lse[row] = L > 0.f ? (x.st.m[0] + log2f(L)) * kLn2f : INFINITY;
+    for (int e = 0; e < 4; ++e) out[16 * dt + e] = (T)(x.st.o[k][dt][e] * inv);
+  if ((lane >> 4) == 0 && a.lse) a.lse[row] = L > 0.f ? (x.st.m[k] + log2f(L)) * kLn2f : INFINITY;
 }
 
 // One piece of the fused append: 16 bytes of the K or V row (kv head kvh)
@@ -225,27 +242,36 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
   const int tspec = table[min(tid, spec_n - 1)];
   const int ti = w / WPT;
   const int h0 = (w % WPT) * 16;
+  // a single (middle) tile is token B's, so that B is always the token that
+  // sees the most keys
   const int iA = tA * TQ + ti;
   const int iB = tB * TQ + ti;
-  const bool actA = iA < q_len;
-  const bool actB = tB != tA && iB < q_len;
+  const bool actA = tB != tA && iA < q_len;
+  const bool actB = iB < q_len;
   const T* __restrict__ q = static_cast<const T*>(a.q);
-  TokenRows<T, D> A, B;
-  A.qrow = actA ? ((int64_t)(q_begin + iA) * a.hq + kvh * G + h0) : -1;
-  B.qrow = actB ? ((int64_t)(q_begin + iB) * a.hq + kvh * G + h0) : -1;
-  load_q<T, D, 1>(A.qf, q, (int64_t)(q_begin + min(iA, q_len - 1)) * a.hq + kvh * G + h0,
-                  lane >> 4, lane & 15);
-  load_q<T, D, 1>(B.qf, q, (int64_t)(q_begin + min(iB, q_len - 1)) * a.hq + kvh * G + h0,
-                  lane >> 4, lane & 15);
-  A.st.reset();
-  B.st.reset();
+  PairRows<T, D> X;
+  X.qrow[0] = actA ? ((int64_t)(q_begin + iA) * a.hq + kvh * G + h0) : -1;
+  X.qrow[1] = actB ? ((int64_t)(q_begin + iB) * a.hq + kvh * G + h0) : -1;
+  {
+    typename Ops<T>::v8 qa[1][D / 32], qb[1][D / 32];
+    load_q<T, D, 1>(qa, q, (int64_t)(q_begin + min(iA, q_len - 1)) * a.hq + kvh * G + h0,
+                    lane >> 4, lane & 15);
+    load_q<T, D, 1>(qb, q, (int64_t)(q_begin + min(iB, q_len - 1)) * a.hq + kvh * G + h0,
+                    lane >> 4, lane & 15);
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      X.qf[0][ks] = qa[0][ks];
+      X.qf[1][ks] = qb[0][ks];
+    }
+  }
+  X.st.reset();
 
   const int cap = a.max_blk << a.bs_shift;
   kv_len = kv_len < cap ? kv_len : cap;
   kv_len = kv_len > 0 ? kv_len : 0;
   const int ctx = a.causal ? max(kv_len - q_len, 0) : 0;
-  A.lim = !actA ? 0 : a.causal ? min(kv_len, ctx + iA + 1) : kv_len;
-  B.lim = !actB ? 0 : a.causal ? min(kv_len, ctx + iB + 1) : kv_len;
+  X.lim[0] = !actA ? 0 : a.causal ? min(kv_len, ctx + iA + 1) : kv_len;
+  X.lim[1] = !actB ? 0 : a.causal ? min(kv_len, ctx + iB + 1) : kv_len;
   // the pair's last token's limit bounds every key either tile reads
   const int kv_hi = a.causal ? min(kv_len, ctx + min(q_len, (tB + 1) * TQ)) : kv_len;
 
@@ -335,7 +361,11 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
     // stage chunk c into LDS buffer c & 1 (free: every wavefront passed the
     // previous barrier after computing chunk c - 2), request chunk c + 2
     // into the same registers, then compute chunk c for both tokens
-    auto step = [&](int c, Piece (&rg)[PER], unsigned& okm) {
+    // chunks [0, cA) are seen by both tokens (A's keys are a prefix of B's),
+    // [cA, nch) by B alone: two phases, each with one compute form
+    const int sa = min(X.lim[0], hi);
+    const int cA = sa > lo ? (sa - lo + kChunk - 1) / kChunk : 0;
+    auto step = [&](int c, Piece (&rg)[PER], unsigned& okm, auto both) {
       char* kl = buf[c & 1];
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
@@ -354,8 +384,7 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
       cx.kl = kl;
       cx.vl = kl + Geo::BYTES;
       cx.seg_lo = lo;
-      token_chunk<T, D>(A, c, lo, hi, cx);
-      token_chunk<T, D>(B, c, lo, hi, cx);
+      pair_chunk<T, D, decltype(both)::value>(X, c, lo, hi, cx);
       if (lo == 0 && c == 0 && dec) {  // its position has arrived: request the table entry
         const int page = d_pos >> a.bs_shift;
         if (d_pos >= 0 && page < a.max_blk)
@@ -364,16 +393,35 @@ __global__ __launch_bounds__(kPBlock, 1) void prefill_mfma_kernel(AttnArgs a) {
     };
     issue(0, rgA, okA);
     issue(1, rgB, okB);
-    for (int c = 0; c < nch; c += 2) {
-      step(c, rgA, okA);
-      if (c + 1 < nch) step(c + 1, rgB, okB);  // uniform across the workgroup
+    // chunk c uses register set c & 1 (its loads were issued two chunks
+    // earlier into the same set); the branches are uniform
+    const std::integral_constant<bool, true> kBoth;
+    const std::integral_constant<bool, false> kOne;
+    int c = 0;
+    for (; c + 1 < cA; c += 2) {
+      step(c, rgA, okA, kBoth);
+      step(c + 1, rgB, okB, kBoth);
+    }
+    if (c < cA) {  // odd cA: its last chunk is even, B alone goes on at an odd one
+      step(c, rgA, okA, kBoth);
+      for (++c; c + 1 < nch; c += 2) {
+        step(c, rgB, okB, kOne);
+        step(c + 1, rgA, okA, kOne);
+      }
+      if (c < nch) step(c, rgB, okB, kOne);
+    } else {
+      for (; c + 1 < nch; c += 2) {
+        step(c, rgA, okA, kOne);
+        step(c + 1, rgB, okB, kOne);
+      }
+      if (c < nch) step(c, rgA, okA, kOne);
     }
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
 
   // ---- finalise the wavefront's 16 rows of each token
-  token_store<T, D>(A, a, lane);
-  token_store<T, D>(B, a, lane);
+  pair_store<T, D>(X, 0, a, lane);
+  pair_store<T, D>(X, 1, a, lane);
   if (fused) {
     if (kv_hi <= 0) {  // no window ran: publish the decode list, request now
       __syncthreads();
