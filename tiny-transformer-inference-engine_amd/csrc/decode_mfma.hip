@@ -59,19 +59,20 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   const T* __restrict__ q = static_cast<const T*>(a.q);
   // Requested before the sequence's metadata arrives: the partition's first
   // table window at the planned partition length (one entry per thread,
-  // entries past the table's end clamped and unused) and, without
-  // query_start_loc, the Q rows (query token s).
+  // entries past the table's end clamped and unused) and the Q rows of query
+  // token s (a decode batch's query_start_loc is 0, 1, 2, ...; when it is
+  // not, the rows are requested again once it has arrived).
   const int spec_blk0 = (part * a.part_tokens) >> a.bs_shift;
   const int tspec = table[max(0, min(spec_blk0 + (int)threadIdx.x, a.max_blk - 1))];
   v8 qf[NT][D / 32];
-  if (!a.qloc) load_q<T, D, NT>(qf, q, (int64_t)s * a.hq + kvh * G, grp, l16);
+  if (s < a.n_tokens) load_q<T, D, NT>(qf, q, (int64_t)s * a.hq + kvh * G, grp, l16);
   TileGeom g;
   if (!tile_geom(a, s, 0, G, g)) return;
   if (part >= g.nparts) return;
   const int kv_lo = part * g.part_len;
   const int kv_hi = min(kv_lo + g.part_len, g.kv_limit);
   const int64_t qrow0 = (int64_t)g.q_begin * a.hq + kvh * G;
-  if (a.qloc) load_q<T, D, NT>(qf, q, qrow0, grp, l16);
+  if (g.q_begin != s) load_q<T, D, NT>(qf, q, qrow0, grp, l16);  // uniform
   // the speculative window is this partition's first one unless the
   // sequence outgrew the planned bound (longer partitions)
   const bool spec_ok = g.part_len == a.part_tokens;
