@@ -29,8 +29,10 @@ using namespace mfma;
 // 4 wavefronts per workgroup, two workgroups per CU: while one workgroup
 // waits on a segment's serial latencies (table slice, Q, partial exchange),
 // the other streams.
-constexpr int kWaves = 4;
-constexpr int kBlock = 64 * kWaves;
+// Wavefronts per workgroup: 8 at D = 128 (one workgroup per CU, two
+// wavefronts per SIMD), 4 at D = 64 (two per CU; an 8-wavefront combination
+// of 16 heads x 64 dims would leave threads without a column).
+constexpr int sk_waves(int d) { return d == 128 ? 8 : 4; }
 
 // Chunks of virtual sequence v (= sequence * hkv + kv head) and its clamped
 // context, from its query_start_loc pair (q0, q1; 0, 1 without
@@ -120,6 +122,7 @@ __device__ __forceinline__ int64_t cut_slot(int ww, int w_first, int r_slot) {
 template <typename T, int G, int D>
 __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, int w_first,
                                           int w_last, int r_slot, int64_t qrow0, int tid) {
+  constexpr int kBlock = 64 * sk_waves(D);
   constexpr int TPH = kBlock / G;
   constexpr int NQ = D / (4 * TPH);
   constexpr int kMB = 4;
@@ -170,7 +173,10 @@ __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, in
 }
 
 template <typename T, int D, int NT, int PF, bool HALVES, bool KV8>
-__global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs k) {
+__global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_kernel(AttnArgs a,
+                                                                                      SkArgs k) {
+  constexpr int kWaves = sk_waves(D);
+  constexpr int kBlock = 64 * kWaves;
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
   constexpr int G = 16 * NT;
@@ -466,7 +472,11 @@ __global__ __launch_bounds__(kBlock, 2) void decode_sk_kernel(AttnArgs a, SkArgs
 
 template <typename T, int D, int NT, int PF, bool HALVES>
 int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
+  constexpr int kBlock = 64 * sk_waves(D);
   k.n_wg = sk_workgroups(D, 16 * NT);
+  // a sequence's fixed cost in chunk units of one workgroup's streaming
+  // time: twice as many wavefronts stream a chunk in half the time
+  k.seg_cost = kSkSegCost * sk_waves(D) / 4;
   if (a.kv8)
     hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, true>), dim3(k.n_wg), dim3(kBlock),
                        0, stream, a, k);
@@ -491,9 +501,8 @@ int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
 }  // namespace
 
 int sk_workgroups(int d, int group) {
-  (void)d;
   (void)group;
-  const int n = 2 * device_cu_count();
+  const int n = 8 / sk_waves(d) * device_cu_count();
   return n < kSkMaxWg ? n : kSkMaxWg;
 }
 

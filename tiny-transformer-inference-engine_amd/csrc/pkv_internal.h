@@ -175,7 +175,8 @@ constexpr int kMaxCounters = (int)((kWsCounterBytes - kWsCtrBytes) / sizeof(int4
 constexpr int kSkMaxWg = 512;  // workgroups of the persistent kernel, at most
 // A sequence's fixed cost in the persistent kernel (Q load, table slice,
 // wavefront merge, output or partial write) measured in 32-token chunks of
-// one workgroup's streaming time.
+// a 4-wavefront workgroup's streaming time (scaled by the launch to its
+// workgroup size).
 constexpr int kSkSegCost = 5;
 // Context bound from which part_tokens = 0 selects the persistent kernel.
 constexpr int kSkAutoKv = 4096;
