@@ -42,30 +42,7 @@ constexpr int kNT = 16;            // output features per tile
 constexpr int kPitch = kNT + 1;    // LDS row pitch of the partial sums (floats)
 constexpr int kKB = 4;             // K steps per wavefront whose loads are in flight together
 
-enum { kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2, kEpiResid = 3, kEpiArgmax = 4 };
-
-// Greedy head (kEpiArgmax): every row's best (logit, feature) so far as one
-// ordered 64-bit key, folded in with atomic max by every tile; the last tile
-// to finish turns the keys into ids and clears them. One set per device,
-// zero between calls (device globals start zeroed and every call leaves
-// them so); calls that overlap on one device race.
-constexpr int kHeadMaxRows = 4096;
-__device__ unsigned long long g_head_keys[kHeadMaxRows];
-__device__ int g_head_count;
-
-// Key order = the framework's argmax order on the rounded logits: a NaN
-// above every number (the first NaN wins), then the larger value, then the
-// smaller index; -0 counts as +0.
-__device__ __forceinline__ unsigned long long head_key(float v, int idx) {
-  unsigned u;
-  if (v != v) {
-    u = 0xffffffffu;
-  } else {
-    const unsigned b = __float_as_uint(v == 0.f ? 0.f : v);
-    u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  }
-  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (unsigned)idx);
-}
+enum { kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2, kEpiResid = 3 };
 
 struct LinArgs {
   void* out;          // plain / swiglu: [m, n] contiguous
@@ -78,8 +55,6 @@ struct LinArgs {
   int k;
   int m_tiles;
   int n_tiles;
-  // greedy head epilogue: argmax ids (nullable: logits only)
-  int64_t* ids;
   // rope epilogue
   void* q_out;
   void* k_out;
@@ -102,31 +77,6 @@ __device__ __forceinline__ float rnd(float x) {
   return (float)(T)fp32_value(x);
 }
 
-// A greedy-head tile's end: once its key updates have completed it counts
-// itself in; the tile that brings the count to the grid size writes every
-// row's id from its key and puts the keys and the count back to zero.
-__device__ __forceinline__ void head_count_in(const LinArgs& a) {
-  __shared__ int s_last;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = fetch_add_agent(&g_head_count, 1);
-    s_last = old == (int)(gridDim.x - 1);
-    if ((old < 0 || old >= (int)gridDim.x) && a.status)
-      atomicOr(a.status, PKV_STATUS_DIRTY_WORKSPACE);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  for (int i = threadIdx.x; i < a.m; i += blockDim.x) {
-    const unsigned long long key =
-        __hip_atomic_load(&g_head_keys[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    a.ids[i] = (int64_t)(0xffffffffu - (unsigned)(key & 0xffffffffull));
-    __hip_atomic_store(&g_head_keys[i], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&g_head_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <typename T, int MB, int EPI, bool NORM>
 __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
 #pragma clang fp contract(off)
@@ -141,12 +91,7 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   const int r = b >> 3;
   const int mt = r % a.m_tiles;
   const int nt = (r / a.m_tiles) * 8 + xcd;
-  if (nt >= a.n_tiles) {  // padding tile: the whole workgroup leaves
-    if constexpr (EPI == kEpiArgmax) {
-      if (a.ids) head_count_in(a);
-    }
-    return;
-  }
+  if (nt >= a.n_tiles) return;  // padding tile: the whole workgroup leaves
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int l16 = lane & 15;
@@ -298,48 +243,6 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
       for (int i = 0; i < 4; ++i) red[s][w][16 * mb + l16][(lane >> 4) * 4 + i] = acc[s][mb][i];
   __syncthreads();
 
-  if constexpr (EPI == kEpiArgmax) {
-    // logits rounded and stored as the plain epilogue does; the row's best
-    // of this tile's 16 features over the row's 8 threads (lanes 8 ml .. +7
-    // of one wavefront), folded into the row's key
-    unsigned long long best = 0ull;
-    if (live) {
-      const bool two = n + 1 < a.n;
-      float v0 = 0.f, v1 = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < kLW; ++ww) {
-        v0 += red[0][ww][ml][2 * p];
-        v1 += red[0][ww][ml][2 * p + 1];
-      }
-      if (a.bias) {
-        const T* bias = static_cast<const T*>(a.bias);
-        v0 = fp32_value(v0 + (float)bias[n]);
-        if (two) v1 = fp32_value(v1 + (float)bias[n + 1]);
-      }
-      const T t0 = (T)v0, t1 = (T)v1;
-      if (a.out) {
-        T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
-        o[0] = t0;
-        if (two) o[1] = t1;
-      }
-      best = head_key((float)t0, n);
-      if (two) {
-        const unsigned long long k1 = head_key((float)t1, n + 1);
-        best = k1 > best ? k1 : best;
-      }
-    }
-    if (a.ids) {
-#pragma unroll
-      for (int off = 1; off < 8; off <<= 1) {
-        const unsigned long long o = __shfl_xor(best, off, 8);
-        best = o > best ? o : best;
-      }
-      if (live && p == 0)
-        __hip_atomic_fetch_max(&g_head_keys[m], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      head_count_in(a);
-    }
-    return;
-  }
   if (!live) return;
   const bool two = n + 1 < a.n;
   float v[NS][2];
@@ -523,35 +426,6 @@ int pkv_linear_swiglu(void* out, const void* x, const void* w_gate_up, const voi
   a.n = (int)n;
   a.k = (int)k;
   return dispatch<kEpiSwiglu>(a, dtype, static_cast<hipStream_t>(stream));
-}
-
-int pkv_lm_head(int64_t* ids, void* logits, const void* x, const void* norm_weight, float eps,
-                const void* w, const void* bias, int64_t m, int64_t n, int64_t k, int64_t x_stride,
-                int dtype, int* status, void* stream) {
-  if (!ids && !logits) return fail(PKV_ERR_INVALID, "lm_head: ids and logits both null");
-  int rc = check_common(ids ? (const void*)ids : logits, x, w, m, n, k, x_stride, dtype);
-  if (rc != PKV_OK) return rc;
-  if (norm_weight && ((uintptr_t)norm_weight & 15))
-    return fail(PKV_ERR_INVALID, "lm_head: norm weight not 16-byte aligned");
-  if (ids && m > kHeadMaxRows)
-    return fail(PKV_ERR_UNSUPPORTED, "lm_head: %lld rows for the greedy choice (at most %d)",
-                (long long)m, kHeadMaxRows);
-  if (m == 0) return PKV_OK;
-  LinArgs a{};
-  a.out = logits;
-  a.ids = ids;
-  a.x = x;
-  a.w = w;
-  a.bias = bias;
-  a.x_stride = x_stride;
-  a.m = (int)m;
-  a.n = (int)n;
-  a.k = (int)k;
-  a.norm_w = norm_weight;
-  a.eps = eps;
-  a.status = status;
-  if (norm_weight) return dispatch<kEpiArgmax, true>(a, dtype, static_cast<hipStream_t>(stream));
-  return dispatch<kEpiArgmax>(a, dtype, static_cast<hipStream_t>(stream));
 }
 
 int pkv_linear_residual(void* resid, const void* x, const void* w, const void* bias, int64_t m,
