@@ -195,16 +195,19 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     } else {
       const int64_t prow = unit * G + cb.head;
       if (a.merge_ctr) {
-        // written through to memory: the merging workgroup may sit on
-        // another XCD
+        // O / sum rounded to fp16 (a weighted mean of value rows, so within
+        // their range: the reference computes in fp16 throughout,
+        // serving/fake_paged_attn.py:208-215) and the fp32 (max, sum):
+        // half the partial traffic of unnormalised fp32 rows. Written
+        // through to memory: the merging workgroup may sit on another XCD.
+        _Float16* po16 = reinterpret_cast<_Float16*>(a.ws_o) + prow * D;
 #pragma unroll
         for (int q = 0; q < Combine::NQ; ++q) {
-          uint64_t b0, b1;
-          __builtin_memcpy(&b0, &cb.acc[q], 8);
-          __builtin_memcpy(&b1, reinterpret_cast<const char*>(&cb.acc[q]) + 8, 8);
-          float* po = a.ws_o + prow * D + cb.col(q);
-          st_agent64(po, b0);
-          st_agent64(po + 2, b1);
+          const half4 h = half4{(_Float16)(cb.acc[q][0] * cb.inv), (_Float16)(cb.acc[q][1] * cb.inv),
+                                (_Float16)(cb.acc[q][2] * cb.inv), (_Float16)(cb.acc[q][3] * cb.inv)};
+          uint64_t b;
+          __builtin_memcpy(&b, &h, 8);
+          st_agent64(po16 + cb.col(q), b);
         }
         if (cb.cq == 0) {
           const float2 ml = make_float2(cb.M, cb.L);
@@ -255,26 +258,30 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   floatx4 acc[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const _Float16* po16 = reinterpret_cast<const _Float16*>(a.ws_o);
   for (int p0 = 0; p0 < g.nparts; p0 += kMB) {
     float2 ml[kMB];
-    floatx4 oo[kMB][NQ];
+    half4 oo[kMB][NQ];
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
       const int64_t row = (unit0 + min(p0 + j, g.nparts - 1)) * G + head;
       ml[j] = *reinterpret_cast<const float2*>(a.ws_ml + row * 2);
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
-        oo[j][q] = *reinterpret_cast<const floatx4*>(a.ws_o + row * D + 4 * (cq + Combine::TPH * q));
+        oo[j][q] = *reinterpret_cast<const half4*>(po16 + row * D + 4 * (cq + Combine::TPH * q));
     }
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
       if (p0 + j >= g.nparts || ml[j].x == -INFINITY) continue;
       const float Mn = fmaxf(M, ml[j].x);
       const float sa = exp2f(M - Mn);
-      const float sb = exp2f(ml[j].x - Mn);
-      L = L * sa + ml[j].y * sb;
+      const float wl = ml[j].y * exp2f(ml[j].x - Mn);  // this partial's weight
+      L = L * sa + wl;
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) acc[q] = acc[q] * sa + oo[j][q] * sb;
+      for (int q = 0; q < NQ; ++q)
+        acc[q] = acc[q] * sa +
+                 floatx4{(float)oo[j][q][0], (float)oo[j][q][1], (float)oo[j][q][2],
+                         (float)oo[j][q][3]} * wl;
       M = Mn;
     }
   }
