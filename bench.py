@@ -28,6 +28,11 @@ Printed JSON line (one):
   north_star     the decode kernel on config 5 (Hq 32, D 128, batch 256,
                  lognormal context mean 1024, fragmented tables), cold: a
                  rotation of 5 seeded problems (1.3 GB of pools);
+                 roofline and north_star also carry plain_read_us: the
+                 library's streaming-read kernel on the same byte count,
+                 cold over as many distinct buffers (the read rate a
+                 kernel that does nothing else reaches on this device), and
+                 frac_of_plain_read = plain_read_us / us_per_launch;
   cfg5_mixed_step  config 5's whole step (256 decodes + 4 new sequences'
                  512-token chunked-prefill append, one fused call) at block
                  sizes 16 and 32, rotated over 3 seeded problems;
@@ -221,9 +226,37 @@ def run_roofline_cfg4(args, torch, st):
     c = cold.time(reps) / L
     w = warm.time(reps) / L
     nbytes = attn_bytes(st["lens"] + 1, st["HQ"], st["HKV"], st["D"], 2, st["BS"])
+    del cold, warm
+    rd = plain_read(nbytes, L, args, torch)
     log(f"cfg4 attention: cold {c * 1e6:.2f} us ({nbytes / c / 1e9:.0f} GB/s), "
-        f"warm {w * 1e6:.2f} us ({nbytes / w / 1e9:.0f} GB/s)")
-    return dict(cold_sec=c, warm_sec=w, bytes=nbytes)
+        f"warm {w * 1e6:.2f} us ({nbytes / w / 1e9:.0f} GB/s); plain read of the same bytes, "
+        f"cold: {rd * 1e6:.2f} us ({nbytes / rd / 1e9:.0f} GB/s)")
+    return dict(cold_sec=c, warm_sec=w, bytes=nbytes, read_sec=rd)
+
+
+def plain_read(nbytes, copies, args, torch):
+    """The device's plain HBM read rate for a kernel that only reads: the
+    library's streaming-read kernel (16-byte non-temporal loads, 4096
+    workgroups) over `copies` distinct buffers of `nbytes` each, one launch
+    per buffer per graph replay, so each buffer was last read copies - 1
+    launches earlier (cold when copies * nbytes exceeds the Infinity Cache).
+    Returns seconds per launch."""
+    from serving import _native
+
+    lib = _native.lib()
+    n16 = (int(nbytes) + 15) // 16 * 16
+    bufs = [torch.empty(n16, dtype=torch.uint8, device="cuda:0").fill_(i + 1)
+            for i in range(copies)]
+
+    def reads():
+        sp = torch.cuda.current_stream().cuda_stream
+        for b in bufs:
+            _native.check(lib.pkv_stream_read(b.data_ptr(), n16, None, 4096, sp), "stream_read")
+    g = Graph(reads)
+    sec = g.time(max(10, args.steps)) / copies
+    del g, bufs
+    torch.cuda.empty_cache()
+    return sec
 
 
 def run_north_star(args, torch):
@@ -251,6 +284,9 @@ def run_north_star(args, torch):
     log(f"cfg5 attention: cold {c * 1e6:.2f} us ({c_gbs:.0f} GB/s, {100 * c_gbs / HBM_PEAK_GBS:.1f}%),"
         f" warm {w * 1e6:.2f} us ({w_gbs:.0f} GB/s)")
     del cold, warm
+    rd = plain_read(sum(nb) / len(nb), len(probs), args, torch)
+    log(f"cfg5: plain read of the same bytes, cold: {rd * 1e6:.2f} us "
+        f"({sum(nb) / len(nb) / rd / 1e9:.0f} GB/s)")
     # the same problems with fp8 pools (CacheConfig.kv_dtype = float8_e4m3fn):
     # half the K/V bytes, Q and O still bf16
     fp8 = torch.float8_e4m3fn
@@ -273,6 +309,9 @@ def run_north_star(args, torch):
            "achieved_gbs": round(c_gbs, 1), "frac_of_peak": round(c_gbs / HBM_PEAK_GBS, 4),
            "warm_us_per_launch": round(w * 1e6, 3), "warm_bytes_per_launch": nb[0],
            "warm_achieved_gbs": round(w_gbs, 1), "target_frac": 0.70,
+           "plain_read_us": round(rd * 1e6, 3),
+           "plain_read_gbs": round(sum(nb) / len(nb) / rd / 1e9, 1),
+           "frac_of_plain_read": round(rd / c, 4),
            "fp8_pools": {"us_per_launch": round(c8 * 1e6, 3),
                          "bytes_per_launch": int(sum(nb8) / len(nb8)),
                          "achieved_gbs": round(g8, 1), "frac_of_peak": round(g8 / HBM_PEAK_GBS, 4),
@@ -798,6 +837,12 @@ def main():
             "us_per_launch": round(roof["cold_sec"] * 1e6, 3),
             "warm_us_per_launch": round(roof["warm_sec"] * 1e6, 3),
             "warm_achieved": round(roof["bytes"] / roof["warm_sec"] / 1e9, 2),
+            "plain_read_us": round(roof["read_sec"] * 1e6, 3),
+            "plain_read_gbs": round(roof["bytes"] / roof["read_sec"] / 1e9, 1),
+            "frac_of_plain_read": round(roof["read_sec"] / roof["cold_sec"], 4),
+            "plain_read": "the library's streaming-read kernel (pkv_stream_read) over 12 "
+                          "distinct buffers of the same byte count in one graph replay: the "
+                          "read rate this device reaches on a kernel that only reads",
         },
         "north_star": ns,
         "cfg5_mixed_step": mixed,

@@ -429,6 +429,16 @@ int pkv_sample_rows(int64_t* ids, const void* logits, int64_t rows, int64_t voca
                     int64_t row_stride, float temperature, int top_k, float top_p,
                     const float* uniforms, int dtype, int* status, void* stream);
 
+/*
+ * Measurement helper, no counterpart in the reference: reads `bytes` bytes at
+ * p (16-byte aligned, a multiple of 16) once with 16-byte non-temporal loads
+ * from `grid` workgroups of 256 threads and writes nothing (sink, nullable,
+ * is written only on an impossible checksum). The benchmark times it on the
+ * same byte counts as the attention kernels to report the device's plain
+ * HBM read rate beside theirs.
+ */
+int pkv_stream_read(const void* p, int64_t bytes, unsigned* sink, int grid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,6 +103,7 @@ _SIGNATURES = {
     "pkv_argmax_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp], _c_int),
     "pkv_sample_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_float,
                          _c_vp, _c_int, _c_vp, _c_vp], _c_int),
+    "pkv_stream_read": ([_c_vp, _c_i64, _c_vp, _c_int, _c_vp], _c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)
