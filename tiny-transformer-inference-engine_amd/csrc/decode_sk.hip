@@ -182,8 +182,8 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
   constexpr int G = 16 * NT;
   constexpr int DT = D / 16;
   constexpr int WAVE_BYTES = 2 * Geo::BYTES;
-  constexpr int OPITCH = D + 4;
-  constexpr int MERGE_BYTES = kWaves * G * OPITCH * 4;
+  using Combine = WaveCombine16<G, D, kWaves, kBlock>;
+  constexpr int MERGE_BYTES = kWaves * G * Combine::OPITCH * 2;
   constexpr int MAIN_BYTES = kWaves * WAVE_BYTES;
   constexpr int LDS_BYTES = MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES;
   __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
   bool bad_block = false;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   T* __restrict__ out = static_cast<T*>(a.out);
-  float* ob = reinterpret_cast<float*>(lds);
+  _Float16* ob = reinterpret_cast<_Float16*>(lds);
   // kTblCap - 1 blocks of tokens: a window that starts inside a block still
   // touches at most kTblCap table entries
   const int win = (kTblCap - 1) << a.bs_shift;
@@ -380,12 +380,17 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
       st.l[nt] = head_lanes_sum(st.l[nt]);
     }
     __syncthreads();
+    // each wavefront's O / l in fp16 (see WaveCombine16)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int nt = 0; nt < NT; ++nt) {
+      const float il = st.l[nt] > 0.f ? 1.f / st.l[nt] : 0.f;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        *reinterpret_cast<floatx4*>(ob + (w * G + 16 * nt + l16) * OPITCH + 16 * dt + 4 * grp) =
-            st.o[nt][dt];
+        *reinterpret_cast<half4*>(ob + (w * G + 16 * nt + l16) * Combine::OPITCH + 16 * dt +
+                                  4 * grp) =
+            half4{(_Float16)(st.o[nt][dt][0] * il), (_Float16)(st.o[nt][dt][1] * il),
+                  (_Float16)(st.o[nt][dt][2] * il), (_Float16)(st.o[nt][dt][3] * il)};
+    }
     if (grp == 0) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
     __syncthreads();
     const int slot = 2 * wg + (first ? 0 : 1);
     {
-      WaveCombine<G, D, kWaves, kBlock> cb;
+      Combine cb;
       cb.run(ob, ml_lds, tid);
       const float inv = cb.inv;
       if (whole) {

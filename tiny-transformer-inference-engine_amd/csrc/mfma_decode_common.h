@@ -608,6 +608,51 @@ struct WaveCombine {
   }
 };
 
+// The same combination with the wavefront states staged as O / l rounded to
+// fp16 (half the LDS bytes of fp32 O; each is a weighted mean of value rows,
+// so within their range: the reference computes in fp16 throughout,
+// serving/fake_paged_attn.py:208-215): ob = [NW][G][OPITCH] halves, ml =
+// [NW][G] (m, l). Wavefront ww's weight is l_ww 2^(m_ww - M).
+template <int G, int D, int NW, int BLOCK>
+struct WaveCombine16 {
+  static constexpr int TPH = BLOCK / G;        // threads per head
+  static constexpr int NQ = D / (4 * TPH);     // 4-column groups per thread
+  static constexpr int OPITCH = D + 8;         // halves
+  static_assert(BLOCK % G == 0 && NQ >= 1 && D % (4 * TPH) == 0, "block / head split");
+  int head, cq;
+  float M, L, inv;  // running max (base 2), sum, 1 / sum (0 when the sum is 0)
+  floatx4 acc[NQ];  // unnormalised output columns
+
+  __device__ __forceinline__ int col(int q) const { return 4 * (cq + TPH * q); }
+
+  __device__ __forceinline__ void run(const _Float16* ob, const float (*ml)[G][2], int tid) {
+    head = tid / TPH;
+    cq = tid - head * TPH;
+    M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, ml[ww][head][0]);
+    L = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
+      float wt[NW];
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        wt[ww] = ml[ww][head][1] * exp2f(ml[ww][head][0] - M);
+        L += wt[ww];
+      }
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const half4 h = *reinterpret_cast<const half4*>(ob + (ww * G + head) * OPITCH + col(q));
+          acc[q] += wt[ww] * floatx4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+        }
+    }
+    inv = L > 0.f ? 1.f / L : 0.f;
+  }
+};
+
 // Fused append of one sequence's query-token row. load_new_row /
 // put_new_row: threads [0, 2 CPR) of the workgroup copy their 16-byte piece
 // of the K / V row `tok` (kv head `kvh`) into the LDS row buffer (the
