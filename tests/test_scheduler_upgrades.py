@@ -149,4 +149,6 @@ def test_reference_mode_unchanged_without_config():
                       block_size=16, top_k=1)
     sched.add_request(list(range(20)), 3)
     res = sched.step()
-    assert [r[0] for r in res] == [0] and sched.running[0]._is_prefill is False
+    seq = sched.running[0]
+    # the prompt is in the pool; the sampled token is next
+    assert [r[0] for r in res] == [0] and sched.computed_tokens(seq) == seq.num_tokens - 1
