@@ -29,10 +29,11 @@ def np64(t):
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def mixed_batch(n_dec, chunks, hq, d, dtype, bs, seed, empty=()):
+def mixed_batch(n_dec, chunks, hq, d, dtype, bs, seed, empty=(), hkv=1, shuffle=False):
     """n_dec decode sequences (lognormal contexts, one new token each) then
     len(chunks) prefill sequences; chunks[i] = (prior context, chunk tokens).
-    Sequences listed in `empty` get no query this step."""
+    Sequences listed in `empty` get no query this step; shuffle: the
+    sequences in a seeded random order instead (decode and prefill mixed)."""
     dec_lens = workloads.lengths_lognormal(n_dec, 600, 3000, seed)
     q_lens, starts = [], []
     for i, L in enumerate(dec_lens):
@@ -41,10 +42,14 @@ def mixed_batch(n_dec, chunks, hq, d, dtype, bs, seed, empty=()):
     for prior, n in chunks:
         q_lens.append(n)
         starts.append(prior)
+    if shuffle:
+        perm = np.random.default_rng(seed).permutation(len(q_lens))
+        q_lens = [q_lens[i] for i in perm]
+        starts = [starts[i] for i in perm]
     ends = [s + q for s, q in zip(starts, q_lens)]
     tables = workloads.permuted_tables([max(e, s + 1) for s, e in zip(starts, ends)], bs,
                                        1 << 15, seed)
-    pool = KVPool(1, bs, 1 << 15, 1, d, dtype, torch.device(DEV))
+    pool = KVPool(1, bs, 1 << 15, hkv, d, dtype, torch.device(DEV))
     g = torch.Generator(device=DEV).manual_seed(seed)
     pool.kv.normal_(generator=g)
     T = sum(q_lens)
@@ -52,8 +57,8 @@ def mixed_batch(n_dec, chunks, hq, d, dtype, bs, seed, empty=()):
     positions = [p for s, q in zip(starts, q_lens) for p in range(s, s + q)]
     meta = pack_batch_meta(tables, qsl, positions, T, torch.device(DEV), bs)
     q = torch.randn(T, hq, d, generator=g, device=DEV).to(dtype)
-    k = torch.randn(T, 1, d, generator=g, device=DEV).to(dtype)
-    v = torch.randn(T, 1, d, generator=g, device=DEV).to(dtype)
+    k = torch.randn(T, hkv, d, generator=g, device=DEV).to(dtype)
+    v = torch.randn(T, hkv, d, generator=g, device=DEV).to(dtype)
     return pool, meta, q, k, v
 
 
@@ -109,3 +114,64 @@ def test_mixed_batch_fused_append_equals_two_calls(bound):
     assert torch.equal(lse_a, lse_b), "lse differs"
     eo, _ = oracle(pool_a, meta, q)
     assert np.abs(np64(out_b) - eo).max() <= 2e-2
+
+
+# The fused mixed call with the persistent decode kernel at head dim 128 runs
+# as one launch (decode shares and prefill pairs in one grid, the decode
+# shares taking their new rows from k_new / v_new); the two-call form runs
+# the same kernels' code on rows read back from the pool. Both are bit for
+# bit the same: every (sequence, kv head) gets the same shares of the
+# persistent kernel's cost line either way.
+@pytest.mark.parametrize("hq,hkv,dtype,bs,shuffle", [
+    (32, 1, torch.bfloat16, 16, False),
+    (32, 1, torch.float16, 32, True),
+    (16, 1, torch.bfloat16, 8, True),
+    (64, 2, torch.bfloat16, 16, True),
+    (32, 2, torch.float16, 16, False),
+], ids=["g32-bf16-bs16", "g32-f16-bs32-shuffled", "g16-bf16-bs8-shuffled",
+        "g32x2-bf16-bs16-shuffled", "g16x2-f16-bs16"])
+def test_mixed_one_launch_equals_two_calls(hq, hkv, dtype, bs, shuffle):
+    print(f"[mixed one launch] hq={hq} hkv={hkv} {dtype} bs={bs} shuffle={shuffle}", flush=True)
+    pool_a, meta, q, k, v = mixed_batch(
+        96, [(0, 128), (0, 77), (500, 128), (0, 1), (0, 256)], hq, 128, dtype, bs, seed=33,
+        empty=(3, 40), hkv=hkv, shuffle=shuffle)
+    meta.max_kv_len = 8192  # the persistent decode kernel
+    pool_b = KVPool(1, bs, pool_a.num_blocks, hkv, 128, dtype, torch.device(DEV))
+    pool_b.kv.copy_(pool_a.kv)
+    lse_a = torch.empty(q.shape[0], hq, device=DEV)
+    lse_b = torch.empty(q.shape[0], hq, device=DEV)
+    pool_a.write_from_table(0, k, v, meta)
+    out_a = paged_attention_meta(q, pool_a.kv[0, 0], pool_a.kv[0, 1], meta, lse=lse_a)
+    out_b = paged_attention_append_meta(q, k, v, pool_b, 0, meta, lse=lse_b)
+    # the same call again: the arrival counters were left at zero
+    out_c = paged_attention_append_meta(q, k, v, pool_b, 0, meta)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a.kv, pool_b.kv), "pools differ"
+    assert torch.equal(out_a, out_b), "outputs differ"
+    assert torch.equal(lse_a, lse_b), "lse differs"
+    assert torch.equal(out_b, out_c), "a repeated call differs"
+    eo, el = oracle(pool_a, meta, q)
+    assert np.abs(np64(out_b) - eo).max() <= 2e-2
+    fin = np.isfinite(el)
+    np.testing.assert_allclose(lse_b.cpu().numpy()[fin], el[fin], rtol=0, atol=2e-2)
+
+
+# max_q_len is a bound: a fused mixed call whose batch holds no sequence
+# with more than one query token still appends every row (the prefill
+# kernel, which appends the decode rows of a mixed batch, has no pair to
+# run), with the two-call form as reference.
+@pytest.mark.parametrize("bound", [0, 8192], ids=["partition", "persistent"])
+def test_mixed_call_without_prefill_rows_still_appends(bound):
+    print(f"[mixed no prefill] bound={bound}", flush=True)
+    pool_a, meta, q, k, v = mixed_batch(40, [], 32, 128, torch.bfloat16, 16, seed=34, empty=(7,))
+    meta.max_q_len = 4
+    if bound:
+        meta.max_kv_len = bound
+    pool_b = KVPool(1, 16, pool_a.num_blocks, 1, 128, torch.bfloat16, torch.device(DEV))
+    pool_b.kv.copy_(pool_a.kv)
+    pool_a.write_from_table(0, k, v, meta)
+    out_a = paged_attention_meta(q, pool_a.kv[0, 0], pool_a.kv[0, 1], meta)
+    out_b = paged_attention_append_meta(q, k, v, pool_b, 0, meta)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a.kv, pool_b.kv), "pools differ"
+    assert torch.equal(out_a, out_b), "outputs differ"

@@ -435,6 +435,23 @@ int device_cu_count() {
   return cache[dev];
 }
 
+SkArgs sk_args_for(const AttnArgs& a) {
+  SkArgs k{};
+  k.n_wg = 2 * device_cu_count() < kSkMaxWg ? 2 * device_cu_count() : kSkMaxWg;
+  k.seg_cost = kSkSegCost;
+  char* ws = reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes;
+  k.recs = reinterpret_cast<int4*>(ws + kWsCtrBytes);
+  k.part_o = reinterpret_cast<_Float16*>(a.ws_o);
+  k.part_ml = reinterpret_cast<float*>(k.part_o + (size_t)kSkMaxWg * 2 * a.group * a.d);
+  return k;
+}
+
+int launch_attention_mixed(const AttnArgs& ad, const AttnArgs& ap, int dtype,
+                           hipStream_t stream) {
+  if (ad.n_seq == 0) return PKV_OK;
+  return launch_mixed_sk(ad, sk_args_for(ad), ap, dtype, stream);
+}
+
 int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
                      hipStream_t stream) {
   if (a.n_seq == 0) return PKV_OK;
@@ -445,16 +462,7 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
   if (p.parts_max > 65535 || p.tiles_max > 65535)
     return fail(PKV_ERR_UNSUPPORTED, "attention grid too large (%d parts, %d tiles, %d seq*hkv)",
                 p.parts_max, p.tiles_max, a.n_seq * a.hkv);
-  if (p.kind == 2) {
-    SkArgs k{};
-    k.n_wg = 2 * device_cu_count() < kSkMaxWg ? 2 * device_cu_count() : kSkMaxWg;
-    k.seg_cost = kSkSegCost;
-    char* ws = reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes;
-    k.recs = reinterpret_cast<int4*>(ws + kWsCtrBytes);
-    k.part_o = reinterpret_cast<_Float16*>(a.ws_o);
-    k.part_ml = reinterpret_cast<float*>(k.part_o + (size_t)kSkMaxWg * 2 * a.group * a.d);
-    return launch_decode_sk(a, k, dtype, stream);
-  }
+  if (p.kind == 2) return launch_decode_sk(a, sk_args_for(a), dtype, stream);
   if (p.kind == 1) {
     if (dtype == PKV_DTYPE_BF16) return launch_mfma<bf16>(a, p, dtype, stream);
     return launch_mfma<f16>(a, p, dtype, stream);

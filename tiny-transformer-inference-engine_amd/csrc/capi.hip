@@ -266,17 +266,25 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     return launch_attention(a, sp.dec, qdtype, (hipStream_t)stream);
   }
   // mixed batch: the decode sequences on an MFMA decode kernel, the
-  // prefill sequences on the prefill kernel. With the fused append the
-  // prefill kernel runs first and appends every row (the decode kernel
-  // after it reads them from the pool); otherwise the prefill rows (and the
-  // decode rows unless the decode kernel takes them fused) are appended
-  // first and the decode kernel runs first.
+  // prefill sequences on the prefill kernel. With the fused append and the
+  // persistent decode kernel (head dim 128) both run in one launch, the
+  // decode shares taking their new rows from k_new / v_new; with the fused
+  // append otherwise the prefill kernel runs first and appends every row
+  // (the decode kernel after it reads them from the pool); without it the
+  // prefill rows (and the decode rows unless the decode kernel takes them
+  // fused) are appended first and the decode kernel runs first.
   AttnArgs ad = args_for(sp.dec, 1);
   AttnArgs ap = args_for(sp.pre, 2);
   if (fuse_pre && sp.pre.kind == 3) {
     ap.k_new = k_new;
     ap.v_new = v_new;
     ap.new_pos = start_pos;
+    if (sp.dec.kind == 2 && mixed_sk_supported(ap, qdtype)) {
+      ad.k_new = k_new;
+      ad.v_new = v_new;
+      ad.new_pos = start_pos;
+      return launch_attention_mixed(ad, ap, qdtype, (hipStream_t)stream);
+    }
     const int rc = launch_attention(ap, sp.pre, qdtype, (hipStream_t)stream);
     if (rc != PKV_OK) return rc;
     return launch_attention(ad, sp.dec, qdtype, (hipStream_t)stream);

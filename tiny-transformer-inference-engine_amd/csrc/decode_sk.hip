@@ -20,6 +20,7 @@
 // The per-chunk pipeline is mfma_decode_common.h. Semantics are those of
 // pagedattn.forward (kernels/pagedattn/pagedattn.cu:142-447) for q_len = 1.
 #include "mfma_decode_common.h"
+#include "prefill_mfma.h"
 
 namespace pkv {
 namespace {
@@ -72,7 +73,8 @@ struct ScanDesc {
   SeqDesc d;
   int q0;  // first query token (its row of q / out)
 };
-__device__ __forceinline__ ScanDesc scan_desc(const AttnArgs& a, int v, const int32_t* alt) {
+__device__ __forceinline__ ScanDesc scan_desc(const AttnArgs& a, int v, const int32_t* alt,
+                                              bool flagger) {
   const int s = v / a.hkv;
   const int32_t* qsrc = a.qloc ? a.qloc : alt;
   const int kl = a.seq_lens[s];
@@ -82,7 +84,7 @@ __device__ __forceinline__ ScanDesc scan_desc(const AttnArgs& a, int v, const in
   r.q0 = a.qloc ? q0 : s;
   const int ql = a.qloc ? q1 - q0 : 1;
   if (a.qloc && ql > 0 && !(a.qfilter == 1 && ql != 1) && (q0 < 0 || q0 + ql > a.n_tokens) &&
-      a.status && blockIdx.x == 0)
+      a.status && flagger)
     atomicOr(a.status, PKV_STATUS_BAD_QLOC);
   r.d = seq_desc(a, r.q0, a.qloc ? q1 : s + 1, kl);
   return r;
@@ -172,32 +174,67 @@ __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, in
   if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
-template <typename T, int D, int NT, int PF, bool HALVES, bool KV8>
-__global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_kernel(AttnArgs a,
-                                                                                      SkArgs k) {
-  constexpr int kWaves = sk_waves(D);
-  constexpr int kBlock = 64 * kWaves;
+// Workgroup geometry and LDS sizes of the persistent kernel.
+template <int D, int NT>
+struct SkGeo {
+  static constexpr int kWaves = sk_waves(D);
+  static constexpr int kBlock = 64 * kWaves;
+  static constexpr int G = 16 * NT;
+  static constexpr int WAVE_BYTES = 2 * ChunkGeo<D>::BYTES;
+  using Combine = WaveCombine16<G, D, kWaves, kBlock>;
+  static constexpr int MERGE_BYTES = kWaves * G * Combine::OPITCH * 2;
+  static constexpr int MAIN_BYTES = kWaves * WAVE_BYTES;
+  // the wavefronts' chunk slices while streaming, the merge area after
+  static constexpr int LDS_BYTES = MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES;
+  static constexpr int ROW_BYTES = 2 * D * 2;  // an appended K and V row (16-bit)
+};
+
+// LDS of one persistent workgroup: pointers to arrays the kernel declares as
+// separate __shared__ objects (so the compiler keeps their accesses apart).
+template <int D, int NT>
+struct SkLds {
+  char* lds;                    // SkGeo::LDS_BYTES, 16-byte aligned
+  float (*ml_lds)[16 * NT][2];  // [kWaves]: the wavefronts' (max, sum) per head
+  int* tbl;                     // kTblCap: the segment's table window
+  int* scan_sh;                 // kBlock: block scans
+  int* sv;                      // 6: the share's first sequence (v, g0, n, kv_len, query
+                                // token) and the last-arriver flag
+  char* nrow;                   // APP: the segment's appended row, K then V (ROW_BYTES)
+};
+
+// Persistent workgroup `wg` of k.n_wg. APP: a mixed-batch launch whose
+// table append runs in the same grid (the prefill workgroups write the
+// decode rows): each sequence's new row, at position new_pos[s], is taken
+// from k_new / v_new (the sequence's query token) in place of its pool row,
+// which may not be written yet; this workgroup writes no pool row.
+template <typename T, int D, int NT, int PF, bool HALVES, bool KV8, bool APP>
+__device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
+                                               const SkLds<D, NT>& sm) {
+  using SG = SkGeo<D, NT>;
+  constexpr int kWaves = SG::kWaves;
+  constexpr int kBlock = SG::kBlock;
   using Geo = ChunkGeo<D>;
   using v8 = typename Ops<T>::v8;
-  constexpr int G = 16 * NT;
+  constexpr int G = SG::G;
   constexpr int DT = D / 16;
-  constexpr int WAVE_BYTES = 2 * Geo::BYTES;
-  using Combine = WaveCombine16<G, D, kWaves, kBlock>;
-  constexpr int MERGE_BYTES = kWaves * G * Combine::OPITCH * 2;
-  constexpr int MAIN_BYTES = kWaves * WAVE_BYTES;
-  constexpr int LDS_BYTES = MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES;
-  __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
-  __shared__ float ml_lds[kWaves][G][2];
-  __shared__ int tbl[kTblCap];
-  __shared__ int scan_sh[kBlock];
-  __shared__ int s_v0, s_g0, s_last, s_n0, s_kl0, s_q0;
+  constexpr int WAVE_BYTES = SG::WAVE_BYTES;
+  using Combine = typename SG::Combine;
+  char* const lds = sm.lds;
+  float(*const ml_lds)[G][2] = sm.ml_lds;
+  int* const tbl = sm.tbl;
+  int* const scan_sh = sm.scan_sh;
+  int& s_v0 = sm.sv[0];
+  int& s_g0 = sm.sv[1];
+  int& s_n0 = sm.sv[2];
+  int& s_kl0 = sm.sv[3];
+  int& s_q0 = sm.sv[4];
+  int& s_last = sm.sv[5];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int grp = lane >> 4;
   const int l16 = lane & 15;
-  const int wg = blockIdx.x;
   const int V = a.n_seq * a.hkv;
 
   // ---- total cost C, then the sequence whose cost interval holds this
@@ -208,7 +245,7 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
   ScanDesc sd_mine{};
   const int32_t* alt = reinterpret_cast<const int32_t*>(k.recs);
   for (int base = 0; base < V; base += kBlock) {
-    const ScanDesc sd = scan_desc(a, min(base + tid, V - 1), alt);
+    const ScanDesc sd = scan_desc(a, min(base + tid, V - 1), alt, wg == 0);
     const int n = base + tid < V ? sk_cost(sd.d.n, K) : 0;
     int ex;
     C += block_scan<kWaves>(n, scan_sh, ex);
@@ -237,7 +274,7 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
     int run = 0;
     for (int base = 0; base < V; base += kBlock) {
       const int v = base + tid;
-      const ScanDesc sd = scan_desc(a, min(v, V - 1), alt);
+      const ScanDesc sd = scan_desc(a, min(v, V - 1), alt, wg == 0);
       const int n = v < V ? sk_cost(sd.d.n, K) : 0;
       int ex;
       const int tot = block_scan<kWaves>(n, scan_sh, ex);
@@ -285,10 +322,19 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
   dsc.n = __builtin_amdgcn_readfirstlane(s_n0);
   dsc.kv_len = __builtin_amdgcn_readfirstlane(s_kl0);
   v8 qf[NT][D / 32];
+  // APP: the segment's appended row (its pieces in registers until staged in
+  // LDS with the segment's first table window) and its position. Requested
+  // for every segment, with the segment's Q: it costs no extra round trip.
+  u32x4 nrp{};
+  int npos = -1;
   {
     const int s = v / a.hkv;
     const int qtok = __builtin_amdgcn_readfirstlane(s_q0);
     load_q<T, D, NT>(qf, q, (int64_t)qtok * a.hq + (v - s * a.hkv) * G, grp, l16);
+    if constexpr (APP) {
+      nrp = load_new_row<D>(a, qtok, v - s * a.hkv, tid);
+      npos = ld_meta(a.new_pos, s);
+    }
   }
   bool first = true;
   bool prestaged = false;  // this segment's first table window (and new row) is in LDS
@@ -325,9 +371,9 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
       nkl = ld_meta(a.seq_lens, sn);
     }
 
-    NewRow nr;  // no appended row: the library appends before this kernel
-    nr.pos = -1;
-    nr.lds = nullptr;
+    NewRow nr;  // APP: staged over its pool row where it falls in this segment
+    nr.pos = APP ? npos : -1;
+    nr.lds = sm.nrow;
     pv.head_off = (int64_t)kvh * D * (KV8 ? 1 : 2);
     const int32_t* __restrict__ table = a.block_tables + (int64_t)s * a.max_blk;
     WaveState<NT, DT> st;
@@ -340,9 +386,10 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
       __syncthreads();  // previous window's table and slices no longer read
       if (!(prestaged && lo == tok_lo)) {  // else staged during the previous segment's merge
         for (int i = tid; i < nblk; i += kBlock) tbl[i] = table[cx.blk_lo + i];
+        if (APP && lo == tok_lo) put_new_row<D>(sm.nrow, nrp, tid);
       }
       __syncthreads();
-      run_chunks<T, D, NT, PF, HALVES, false, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
+      run_chunks<T, D, NT, PF, HALVES, APP, KV8>(w, kWaves, cx, pv, qf, st, bad_block, nr);
     }
 
     // ---- the next segment: its Q and first table window are loaded now
@@ -366,6 +413,11 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
     const int kvh_n = v_sel - s_n * a.hkv;
     const int qtok_n = a.qloc ? ld_meta(a.qloc, s_n) : s_n;
     load_q<T, D, NT>(qf, q, (int64_t)qtok_n * a.hq + kvh_n * G, grp, l16);
+    int npos_n = -1;
+    if constexpr (APP) {
+      nrp = load_new_row<D>(a, qtok_n, kvh_n, tid);
+      npos_n = ld_meta(a.new_pos, s_n);
+    }
     const int c1_n = min(d_n.n, end - (g0_n + K));
     const int tok_hi_n = min(c1_n * kChunk, d_n.kv_len);
     const int n_nblk =
@@ -465,14 +517,93 @@ __global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_k
     }
     __syncthreads();  // LDS merge area, table and row buffer are free
     if (!has_next) break;
-    if (tid < n_nblk) tbl[tid] = tpref;  // published by the window loop's first barrier
+    // published by the window loop's first barrier
+    if (tid < n_nblk) tbl[tid] = tpref;
+    if constexpr (APP) put_new_row<D>(sm.nrow, nrp, tid);
     prestaged = true;
     v = v_n;
     g0 = g0_n;
     dsc = d_n;
+    npos = npos_n;
     first = false;
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
+}
+
+template <typename T, int D, int NT, int PF, bool HALVES, bool KV8>
+__global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_kernel(AttnArgs a,
+                                                                                      SkArgs k) {
+  using SG = SkGeo<D, NT>;
+  __shared__ __attribute__((aligned(16))) char lds[SG::LDS_BYTES];
+  __shared__ float ml_lds[SG::kWaves][SG::G][2];
+  __shared__ int tbl[kTblCap];
+  __shared__ int scan_sh[SG::kBlock];
+  __shared__ int sv[6];
+  const SkLds<D, NT> sm{lds, ml_lds, tbl, scan_sh, sv, nullptr};
+  decode_sk_body<T, D, NT, PF, HALVES, KV8, false>(a, k, blockIdx.x, sm);
+}
+
+// A mixed batch in one launch (D = 128, 16-bit pools): workgroups
+// [0, k.n_wg) are the persistent decode kernel's shares over the one-token
+// sequences (ad: qfilter 1, each new row taken from k_new), the rest the
+// prefill kernel's pair workgroups over the others, pair slot i % pre_slots
+// of kv head i / pre_slots (ap: qfilter 2, with the fused append of every
+// row of the batch). No workgroup reads what another writes in this launch:
+// the decode shares never read their new rows' pool slots' contents (they
+// are overwritten in LDS), and the prefill pairs read their own new rows from
+// k_new / v_new. Dispatched in order, the decode shares fill the CUs first,
+// and each pair workgroup starts on a CU as soon as a share there has
+// ended, so the prefill's prologue and the decode shares' uneven ends
+// overlap instead of adding up across two launches. (Pair workgroups that
+// walk several slots, so that the grid holds no empty ones, measured
+// slower: the loop costs the kernel 10 spilled VGPRs.)
+template <typename T, int NT, bool HALVES>
+__global__ __launch_bounds__(kPBlock, 1) void mixed_sk_kernel(AttnArgs ad, SkArgs k, AttnArgs ap,
+                                                              int pre_slots) {
+  constexpr int D = 128;
+  using SG = SkGeo<D, NT>;
+  static_assert(SG::kBlock == kPBlock, "one workgroup size for both parts");
+  constexpr int kLdsBytes =
+      SG::LDS_BYTES > PrefillLds<D>::kBufBytes ? SG::LDS_BYTES : PrefillLds<D>::kBufBytes;
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  __shared__ float ml_lds[SG::kWaves][SG::G][2];
+  __shared__ int tbl[kTblCap];
+  __shared__ int scan_sh[SG::kBlock];
+  __shared__ int sv[6];
+  __shared__ __attribute__((aligned(16))) char nrow[SG::ROW_BYTES];
+  __shared__ int dl_seq[kPBlock], dl_tok[kPBlock];
+  const int b = blockIdx.x;
+  if (b < k.n_wg) {
+    const SkLds<D, NT> sm{lds, ml_lds, tbl, scan_sh, sv, nrow};
+    decode_sk_body<T, D, NT, 1, HALVES, false, true>(ad, k, b, sm);
+  } else {
+    const PrefillLds<D> sm{lds, tbl, scan_sh, sv, dl_seq, dl_tok};
+    const int i = b - k.n_wg;
+    prefill_pair_body<T, D, NT, false, false>(ap, i % pre_slots, i / pre_slots, sm);
+  }
+}
+
+template <typename T, int NT, bool HALVES>
+int launch_mixed_v(const AttnArgs& ad, SkArgs k, const AttnArgs& ap, hipStream_t stream) {
+  k.n_wg = sk_workgroups(128, 16 * NT);
+  k.seg_cost = kSkSegCost * sk_waves(128) / 4;
+  const int64_t slots = prefill_slots(ap.n_tokens, ap.n_seq, ap.group);
+  const int64_t grid = k.n_wg + slots * ap.hkv;
+  if (grid > 0x7fffffff)
+    return fail(PKV_ERR_UNSUPPORTED, "mixed_sk: %lld workgroups", (long long)grid);
+  hipLaunchKernelGGL((mixed_sk_kernel<T, NT, HALVES>), dim3((unsigned)grid), dim3(kPBlock), 0,
+                     stream, ad, k, ap, (int)slots);
+  return check_launch("mixed_sk_kernel");
+}
+
+template <typename T>
+int launch_mixed_t(const AttnArgs& ad, const SkArgs& k, const AttnArgs& ap, hipStream_t stream) {
+  const bool halves = ad.bs_shift >= 4;
+  if (ad.group == 16)
+    return halves ? launch_mixed_v<T, 1, true>(ad, k, ap, stream)
+                  : launch_mixed_v<T, 1, false>(ad, k, ap, stream);
+  return halves ? launch_mixed_v<T, 2, true>(ad, k, ap, stream)
+                : launch_mixed_v<T, 2, false>(ad, k, ap, stream);
 }
 
 template <typename T, int D, int NT, int PF, bool HALVES>
@@ -509,6 +640,21 @@ int sk_workgroups(int d, int group) {
   (void)group;
   const int n = 8 / sk_waves(d) * device_cu_count();
   return n < kSkMaxWg ? n : kSkMaxWg;
+}
+
+bool mixed_sk_supported(const AttnArgs& ap, int dtype) {
+  return (dtype == PKV_DTYPE_BF16 || dtype == PKV_DTYPE_F16) && ap.d == 128 &&
+         (ap.group == 16 || ap.group == 32) && !ap.kv8 && ap.k_new && ap.v_new && ap.new_pos &&
+         ap.qloc && ap.max_blk >= 1 && ap.num_blocks < (int64_t(1) << 31) &&
+         ap.n_seq <= kPrefillFuseMaxSeq && !pool_needs_off64(ap);
+}
+
+int launch_mixed_sk(const AttnArgs& ad, const SkArgs& k, const AttnArgs& ap, int dtype,
+                    hipStream_t stream) {
+  if (!mixed_sk_supported(ap, dtype) || !ad.k_new || !ad.new_pos)
+    return fail(PKV_ERR_UNSUPPORTED, "mixed_sk: d=%d group=%d dtype %d", ap.d, ap.group, dtype);
+  if (dtype == PKV_DTYPE_BF16) return launch_mixed_t<bf16>(ad, k, ap, stream);
+  return launch_mixed_t<f16>(ad, k, ap, stream);
 }
 
 int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream) {

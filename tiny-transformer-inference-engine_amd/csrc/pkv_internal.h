@@ -319,6 +319,22 @@ int launch_decode_mfma(const AttnArgs& a, const AttnPlan& plan, int dtype,
 // Workgroups the persistent kernel launches for this head shape.
 int sk_workgroups(int d, int group);
 int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream);
+// A mixed batch in one launch (decode_sk.hip): the persistent decode shares
+// (ad, qfilter 1) and the MFMA prefill pairs with the fused append (ap,
+// qfilter 2) as workgroups of one grid. Supported for bf16/fp16 16-bit
+// pools, head dim 128, 16 or 32 query heads per kv head, pools addressed
+// with 32-bit offsets; ad and ap carry k_new / v_new / new_pos.
+bool mixed_sk_supported(const AttnArgs& ap, int dtype);
+int launch_mixed_sk(const AttnArgs& ad, const SkArgs& k, const AttnArgs& ap, int dtype,
+                    hipStream_t stream);
+// The persistent kernel's arguments for launch view a (workspace layout:
+// arrival records after the counter header, then the partials).
+SkArgs sk_args_for(const AttnArgs& a);
+// launch_attention for a mixed batch whose decode part is planned on the
+// persistent kernel and whose prefill part takes the fused append, when
+// mixed_sk_supported(ap): one launch.
+int launch_attention_mixed(const AttnArgs& ad, const AttnArgs& ap, int dtype,
+                           hipStream_t stream);
 // CUs of the current device (cached; 256 when no device is visible).
 int device_cu_count();
 
