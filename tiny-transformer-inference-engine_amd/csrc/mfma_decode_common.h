@@ -414,8 +414,12 @@ __device__ __forceinline__ void chunk_update_sub(int c, const ChunkCtx& cx,
   // shuffles and the rescale of l and O) when some score of the wavefront
   // exceeds it by more than kLazy; so p <= 2^kLazy, exact in bf16/fp16
   // relative terms, and most chunks skip the shuffles and the rescale.
-  // P^T operand = this lane's 8 probabilities.
+  // P^T operand = this lane's 8 probabilities. The scores stay unscaled
+  // (masked ones -inf): the scale c = softmax scale * log2(e) > 0 is applied
+  // to the row maximum (max(s) c = max(s c) exactly, rounding being
+  // monotone) and inside each exponent's fma, p = 2^(s c - m).
   const int cb = cx.seg_lo + c * kChunk;
+  const float sc = cx.scale_log2;
   float sv[NC][8];
   bool move = false;
 #pragma unroll
@@ -427,12 +431,11 @@ __device__ __forceinline__ void chunk_update_sub(int c, const ChunkCtx& cx,
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const float x =
-            !MASK || 16 * h + rr < lim ? sacc[nt][h][rr] * cx.scale_log2 : -INFINITY;
+        const float x = !MASK || 16 * h + rr < lim ? sacc[nt][h][rr] : -INFINITY;
         sv[nt][4 * h + rr] = x;
         mx = fmaxf(mx, x);
       }
-    move |= mx > st.m[N0 + nt] + kLazy;  // also true on the first scores (m = -inf)
+    move |= mx * sc > st.m[N0 + nt] + kLazy;  // also true on the first scores (m = -inf)
   }
   if (__builtin_amdgcn_ballot_w64(move) != 0) {
 #pragma unroll
@@ -440,7 +443,7 @@ __device__ __forceinline__ void chunk_update_sub(int c, const ChunkCtx& cx,
       float mx = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sv[nt][e]);
-      mx = head_lanes_max(mx);
+      mx = head_lanes_max(mx) * sc;
       const float m_new = fmaxf(st.m[N0 + nt], mx);
       const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(st.m[N0 + nt] - m_new);
       st.l[N0 + nt] *= alpha;
@@ -452,11 +455,11 @@ __device__ __forceinline__ void chunk_update_sub(int c, const ChunkCtx& cx,
   v8 pf[NC];
 #pragma unroll
   for (int nt = 0; nt < NC; ++nt) {
-    const float ref = st.m[N0 + nt] == -INFINITY ? 0.f : st.m[N0 + nt];
+    const float nref = st.m[N0 + nt] == -INFINITY ? 0.f : -st.m[N0 + nt];
     float ps = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float p = exp2_fast(sv[nt][e] - ref);
+      const float p = exp2_fast(__builtin_fmaf(sv[nt][e], sc, nref));
       ps += p;
       pf[nt][e] = (T)p;
     }
