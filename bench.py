@@ -36,6 +36,10 @@ Printed JSON line (one):
   cfg5_mixed_step  config 5's whole step (256 decodes + 4 new sequences'
                  512-token chunked-prefill append, one fused call) at block
                  sizes 16 and 32, rotated over 3 seeded problems;
+                 roofline, north_star, their plain reads and
+                 cfg5_mixed_step are each the median of 3 timings of the
+                 same graph (the first timing after a capture often runs a
+                 few percent slow);
   decode_tok_s   the full config-4 model decode step (projections, this
                  path, greedy argmax) replayed from one HIP graph;
   configs        cfg1 (fp32 greedy model step), cfg2 (decode op, fp32 and
@@ -133,11 +137,17 @@ class Graph:
     def replay(self):
         self.g.replay()
 
-    def time(self, replays, warm=3):
+    def time(self, replays, warm=3, repeats=1):
+        """Seconds per replay over `replays` replays after `warm` untimed
+        ones; with repeats > 1, the median of that many such timings (the
+        first timing after a capture often runs a few percent slow)."""
+        import statistics
         import torch
         for _ in range(warm):
             self.g.replay()
-        return time_events(self.g.replay, replays, torch.cuda.current_stream())
+        ts = [time_events(self.g.replay, replays, torch.cuda.current_stream())
+              for _ in range(max(1, repeats))]
+        return statistics.median(ts)
 
 
 def cfg4_tables(lens, bs, num_blocks, extra_tokens, seed):
@@ -223,8 +233,8 @@ def run_roofline_cfg4(args, torch, st):
     warm = Graph(lambda: [paged_attention_meta(q, pool.kv[0, 0], pool.kv[0, 1], meta, out=out)
                           for _ in range(L)])
     reps = max(10, args.steps)
-    c = cold.time(reps) / L
-    w = warm.time(reps) / L
+    c = cold.time(reps, repeats=3) / L
+    w = warm.time(reps, repeats=3) / L
     nbytes = attn_bytes(st["lens"] + 1, st["HQ"], st["HKV"], st["D"], 2, st["BS"])
     del cold, warm
     rd = plain_read(nbytes, L, args, torch)
@@ -253,7 +263,7 @@ def plain_read(nbytes, copies, args, torch):
         for b in bufs:
             _native.check(lib.pkv_stream_read(b.data_ptr(), n16, None, 4096, sp), "stream_read")
     g = Graph(reads)
-    sec = g.time(max(10, args.steps)) / copies
+    sec = g.time(max(10, args.steps), repeats=3) / copies
     del g, bufs
     torch.cuda.empty_cache()
     return sec
@@ -276,8 +286,8 @@ def run_north_star(args, torch):
     cold = Graph(lambda: [launch(i) for i in range(len(probs))])
     warm = Graph(lambda: [launch(0) for _ in range(len(probs))])
     reps = max(10, args.steps)
-    c = cold.time(reps) / len(probs)
-    w = warm.time(reps) / len(probs)
+    c = cold.time(reps, repeats=3) / len(probs)
+    w = warm.time(reps, repeats=3) / len(probs)
     nb = [attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs) for p in probs]
     c_gbs = sum(nb) / len(nb) / c / 1e9
     w_gbs = nb[0] / w / 1e9
@@ -295,7 +305,7 @@ def run_north_star(args, torch):
         p.v_pool = p.v_pool.to(fp8)
     torch.cuda.empty_cache()
     cold8 = Graph(lambda: [launch(i) for i in range(len(probs))])
-    c8 = cold8.time(reps) / len(probs)
+    c8 = cold8.time(reps, repeats=3) / len(probs)
     nb8 = [attn_bytes(p.lens, p.hq, p.hkv, p.d, 2, p.bs, kv_esize=1) for p in probs]
     g8 = sum(nb8) / len(nb8) / c8 / 1e9
     log(f"cfg5 attention, fp8 pools: cold {c8 * 1e6:.2f} us ({g8:.0f} GB/s, "
@@ -354,7 +364,7 @@ def run_mixed_step(args, torch):
             p = probs[i]
             paged_attention_append_meta(p.q, p.k, p.v, p.pool, 0, p.meta, out=outs[i])
         graph = Graph(lambda: [step(i) for i in range(len(probs))])
-        sec = graph.time(max(10, args.steps)) / len(probs)
+        sec = graph.time(max(10, args.steps), repeats=3) / len(probs)
         nbytes = sum(mixed_step_bytes(p.dec_lens, chunk, p.n_new, bs=bs) for p in probs) / len(probs)
         gbs = nbytes / sec / 1e9
         log(f"cfg5 mixed step bs {bs} (256 decode + 4 x {chunk} prefill): {sec * 1e6:.1f} us, "
