@@ -221,14 +221,20 @@ int pkv_paged_attention(void* out, float* lse, const void* q,
  * pkv_append_from_table followed by pkv_paged_attention in one call: the
  * step's new K/V rows (k_new, v_new [n_tokens, hkv, d], row t of sequence s
  * at position start_pos[s] + t - query_start_loc[s]) are appended to the
- * pools and attended to by the same call. On the split-K partition decode
- * kernel (bf16/f16, one query per sequence, 16 or 32 query heads per kv
- * head, d = 64 or 128, context bound below 4096 tokens) the append is fused
- * into the attention launch: the workgroup whose context range covers the
- * new row takes it from k_new / v_new and the one holding the sequence's
- * last chunk writes it to its pool slot; elsewhere (persistent decode,
- * prefill and mixed batches' prefill rows, generic kernel) the table append
- * runs first. Same results, status bits and pool contents as the two calls.
+ * pools and attended to by the same call. The append is fused into the
+ * attention launch where the kernel allows: on the split-K partition decode
+ * kernel (bf16/f16 queries, one query per sequence, 16 or 32 query heads per
+ * kv head, d = 64 or 128, context bound below 4096 tokens; fp8 pools too)
+ * the workgroup whose context range covers the new row takes it from k_new
+ * / v_new and the one holding the sequence's last chunk writes it to its
+ * pool slot; with 16-bit pools, the MFMA prefill kernel (at most 512
+ * sequences) writes every row of its batch, a mixed batch's decode rows
+ * included, and reads its own new rows from k_new / v_new, and a mixed batch
+ * whose decode part runs on the persistent kernel at d = 128 runs as one
+ * launch, the decode workgroups taking their new rows from k_new / v_new.
+ * Elsewhere (persistent decode alone, prefill on fp8 pools, generic kernel)
+ * the table append runs first. Same results, status bits and pool contents
+ * as the two calls.
  * query_start_loc is required.
  * Replaces KVPool.write + paged_varlen_attention as called per layer in
  * MQA_Paged.forward_paged_batched (serving/paged_mqa.py:98-110).
