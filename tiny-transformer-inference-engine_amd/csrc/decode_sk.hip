@@ -1,5 +1,5 @@
-// Paged MQA decode, persistent form: two 4-wavefront workgroups per CU, each
-// owning an equal share of all sequences' work.
+// Paged MQA decode, persistent form: one workgroup per CU (two at head dim
+// 64), each owning an equal share of all sequences' work.
 //
 // Every (sequence, kv head) pair v with a query is laid end to end on a cost
 // line as K overhead units (its Q load, table slice, wavefront merge and
@@ -27,12 +27,12 @@ namespace {
 
 using namespace mfma;
 
-// 4 wavefronts per workgroup, two workgroups per CU: while one workgroup
-// waits on a segment's serial latencies (table slice, Q, partial exchange),
-// the other streams.
-// Wavefronts per workgroup: 8 at D = 128 (one workgroup per CU, two
-// wavefronts per SIMD), 4 at D = 64 (two per CU; an 8-wavefront combination
-// of 16 heads x 64 dims would leave threads without a column).
+// Wavefronts per workgroup: at D = 64, 4 (two workgroups per CU; an
+// 8-wavefront combination of 16 heads x 64 dims would leave threads without a
+// column); at D = 128, 4 for a batch of decode sequences alone (one
+// workgroup per CU, at most 256 VGPRs) and 8 for the decode part of a mixed
+// batch, the size of the one-launch mixed kernel's workgroups (so that both
+// forms of a mixed call give the same results).
 constexpr int sk_waves(int d) { return d == 128 ? 8 : 4; }
 
 // Chunks of virtual sequence v (= sequence * hkv + kv head) and its clamped
@@ -121,10 +121,10 @@ __device__ __forceinline__ int64_t cut_slot(int ww, int w_first, int r_slot) {
 // its head is read once per contributor, and every load of a batch of kMB
 // contributors is issued before any is consumed. Loads are device-coherent (they bypass this XCD's L2:
 // the partials were written through from other XCDs during this launch).
-template <typename T, int G, int D>
+template <typename T, int G, int D, int NW>
 __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, int w_first,
                                           int w_last, int r_slot, int64_t qrow0, int tid) {
-  constexpr int kBlock = 64 * sk_waves(D);
+  constexpr int kBlock = 64 * NW;
   constexpr int TPH = kBlock / G;
   constexpr int NQ = D / (4 * TPH);
   constexpr int kMB = 4;
@@ -174,10 +174,11 @@ __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, in
   if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
-// Workgroup geometry and LDS sizes of the persistent kernel.
-template <int D, int NT>
+// Workgroup geometry and LDS sizes of the persistent kernel with NW
+// wavefronts per workgroup.
+template <int D, int NT, int NW>
 struct SkGeo {
-  static constexpr int kWaves = sk_waves(D);
+  static constexpr int kWaves = NW;
   static constexpr int kBlock = 64 * kWaves;
   static constexpr int G = 16 * NT;
   static constexpr int WAVE_BYTES = 2 * ChunkGeo<D>::BYTES;
@@ -202,15 +203,15 @@ struct SkLds {
   char* nrow;                   // APP: the segment's appended row, K then V (ROW_BYTES)
 };
 
-// Persistent workgroup `wg` of k.n_wg. APP: a mixed-batch launch whose
+// Persistent workgroup `wg` of k.n_wg, NW wavefronts. APP: a mixed-batch launch whose
 // table append runs in the same grid (the prefill workgroups write the
 // decode rows): each sequence's new row, at position new_pos[s], is taken
 // from k_new / v_new (the sequence's query token) in place of its pool row,
 // which may not be written yet; this workgroup writes no pool row.
-template <typename T, int D, int NT, int PF, bool HALVES, bool KV8, bool APP>
+template <typename T, int D, int NT, int PF, bool HALVES, bool KV8, bool APP, int NW>
 __device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
                                                const SkLds<D, NT>& sm) {
-  using SG = SkGeo<D, NT>;
+  using SG = SkGeo<D, NT, NW>;
   constexpr int kWaves = SG::kWaves;
   constexpr int kBlock = SG::kBlock;
   using Geo = ChunkGeo<D>;
@@ -512,7 +513,7 @@ __device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
       }
       __syncthreads();
       if (s_last)
-        merge_cut<T, G, D>(a, k, w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0,
+        merge_cut<T, G, D, kWaves>(a, k, w_first, w_last, share_start(w_first, C, W) < g0 ? 1 : 0,
                            qrow0, tid);
     }
     __syncthreads();  // LDS merge area, table and row buffer are free
@@ -530,17 +531,16 @@ __device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
 }
 
-template <typename T, int D, int NT, int PF, bool HALVES, bool KV8>
-__global__ __launch_bounds__(64 * sk_waves(D), 8 / sk_waves(D)) void decode_sk_kernel(AttnArgs a,
-                                                                                      SkArgs k) {
-  using SG = SkGeo<D, NT>;
+template <typename T, int D, int NT, int PF, bool HALVES, bool KV8, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void decode_sk_kernel(AttnArgs a, SkArgs k) {
+  using SG = SkGeo<D, NT, NW>;
   __shared__ __attribute__((aligned(16))) char lds[SG::LDS_BYTES];
   __shared__ float ml_lds[SG::kWaves][SG::G][2];
   __shared__ int tbl[kTblCap];
   __shared__ int scan_sh[SG::kBlock];
   __shared__ int sv[6];
   const SkLds<D, NT> sm{lds, ml_lds, tbl, scan_sh, sv, nullptr};
-  decode_sk_body<T, D, NT, PF, HALVES, KV8, false>(a, k, blockIdx.x, sm);
+  decode_sk_body<T, D, NT, PF, HALVES, KV8, false, NW>(a, k, blockIdx.x, sm);
 }
 
 // A mixed batch in one launch (D = 128, 16-bit pools): workgroups
@@ -561,7 +561,7 @@ template <typename T, int NT, bool HALVES>
 __global__ __launch_bounds__(kPBlock, 1) void mixed_sk_kernel(AttnArgs ad, SkArgs k, AttnArgs ap,
                                                               int pre_slots) {
   constexpr int D = 128;
-  using SG = SkGeo<D, NT>;
+  using SG = SkGeo<D, NT, sk_waves(D)>;
   static_assert(SG::kBlock == kPBlock, "one workgroup size for both parts");
   constexpr int kLdsBytes =
       SG::LDS_BYTES > PrefillLds<D>::kBufBytes ? SG::LDS_BYTES : PrefillLds<D>::kBufBytes;
@@ -575,7 +575,7 @@ __global__ __launch_bounds__(kPBlock, 1) void mixed_sk_kernel(AttnArgs ad, SkArg
   const int b = blockIdx.x;
   if (b < k.n_wg) {
     const SkLds<D, NT> sm{lds, ml_lds, tbl, scan_sh, sv, nrow};
-    decode_sk_body<T, D, NT, 1, HALVES, false, true>(ad, k, b, sm);
+    decode_sk_body<T, D, NT, 1, HALVES, false, true, sk_waves(D)>(ad, k, b, sm);
   } else {
     const PrefillLds<D> sm{lds, tbl, scan_sh, sv, dl_seq, dl_tok};
     const int i = b - k.n_wg;
@@ -586,7 +586,7 @@ __global__ __launch_bounds__(kPBlock, 1) void mixed_sk_kernel(AttnArgs ad, SkArg
 template <typename T, int NT, bool HALVES>
 int launch_mixed_v(const AttnArgs& ad, SkArgs k, const AttnArgs& ap, hipStream_t stream) {
   k.n_wg = sk_workgroups(128, 16 * NT);
-  k.seg_cost = kSkSegCost * sk_waves(128) / 4;
+  k.seg_cost = kSkSegCost * sk_waves(128) / 4;  // see launch_v
   const int64_t slots = prefill_slots(ap.n_tokens, ap.n_seq, ap.group);
   const int64_t grid = k.n_wg + slots * ap.hkv;
   if (grid > 0x7fffffff)
@@ -606,18 +606,18 @@ int launch_mixed_t(const AttnArgs& ad, const SkArgs& k, const AttnArgs& ap, hipS
                 : launch_mixed_v<T, 2, false>(ad, k, ap, stream);
 }
 
-template <typename T, int D, int NT, int PF, bool HALVES>
+template <typename T, int D, int NT, int PF, bool HALVES, int NW>
 int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
-  constexpr int kBlock = 64 * sk_waves(D);
+  constexpr int kBlock = 64 * NW;
   k.n_wg = sk_workgroups(D, 16 * NT);
   // a sequence's fixed cost in chunk units of one workgroup's streaming
   // time: twice as many wavefronts stream a chunk in half the time
-  k.seg_cost = kSkSegCost * sk_waves(D) / 4;
+  k.seg_cost = kSkSegCost * NW / 4;
   if (a.kv8)
-    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, true>), dim3(k.n_wg), dim3(kBlock),
-                       0, stream, a, k);
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, true, NW>), dim3(k.n_wg),
+                       dim3(kBlock), 0, stream, a, k);
   else
-    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, false>), dim3(k.n_wg),
+    hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, false, NW>), dim3(k.n_wg),
                        dim3(kBlock), 0, stream, a, k);
   return check_launch("decode_sk_kernel");
 }
@@ -625,12 +625,21 @@ int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
 template <typename T, bool HALVES>
 int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
   const int nt = a.group / 16;
-  // <T, D, NT, PF, HALVES>: two wavefronts per SIMD; the D = 128 variants
-  // have room for one chunk in flight per wavefront, the D = 64 ones for two
-  if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, HALVES>(a, k, stream);
-  if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, HALVES>(a, k, stream);
-  if (a.d == 128 && nt == 1) return launch_v<T, 128, 1, 1, HALVES>(a, k, stream);
-  if (a.d == 128 && nt == 2) return launch_v<T, 128, 2, 1, HALVES>(a, k, stream);
+  // <T, D, NT, PF, HALVES, NW>: the D = 128 variants have room for one
+  // chunk in flight per wavefront, the D = 64 ones for two. At D = 128 a
+  // batch of decode sequences alone runs 4-wavefront workgroups, one per CU
+  // (cfg5: 33.8 against 34.7 us for 8 wavefronts); the decode part of a
+  // mixed batch (qfilter 1) 8-wavefront ones, as in the one-launch mixed
+  // kernel.
+  const bool mixed = a.qfilter == 1;
+  if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, HALVES, 4>(a, k, stream);
+  if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, HALVES, 4>(a, k, stream);
+  if (a.d == 128 && nt == 1)
+    return mixed ? launch_v<T, 128, 1, 1, HALVES, 8>(a, k, stream)
+                 : launch_v<T, 128, 1, 1, HALVES, 4>(a, k, stream);
+  if (a.d == 128 && nt == 2)
+    return mixed ? launch_v<T, 128, 2, 1, HALVES, 8>(a, k, stream)
+                 : launch_v<T, 128, 2, 1, HALVES, 4>(a, k, stream);
   return fail(PKV_ERR_UNSUPPORTED, "decode_sk: d=%d group=%d", a.d, a.group);
 }
 
@@ -638,7 +647,8 @@ int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
 
 int sk_workgroups(int d, int group) {
   (void)group;
-  const int n = 8 / sk_waves(d) * device_cu_count();
+  // one workgroup per CU at D = 128 (4 or 8 wavefronts), two at D = 64
+  const int n = (d == 128 ? 1 : 2) * device_cu_count();
   return n < kSkMaxWg ? n : kSkMaxWg;
 }
 
