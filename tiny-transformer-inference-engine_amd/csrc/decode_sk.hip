@@ -586,7 +586,7 @@ __global__ __launch_bounds__(kPBlock, 1) void mixed_sk_kernel(AttnArgs ad, SkArg
 template <typename T, int NT, bool HALVES>
 int launch_mixed_v(const AttnArgs& ad, SkArgs k, const AttnArgs& ap, hipStream_t stream) {
   k.n_wg = sk_workgroups(128, 16 * NT);
-  k.seg_cost = kSkSegCost * sk_waves(128) / 4;  // see launch_v
+  k.seg_cost = kSkSegCost128(sk_waves(128));
   const int64_t slots = prefill_slots(ap.n_tokens, ap.n_seq, ap.group);
   const int64_t grid = k.n_wg + slots * ap.hkv;
   if (grid > 0x7fffffff)
@@ -611,8 +611,9 @@ int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
   constexpr int kBlock = 64 * NW;
   k.n_wg = sk_workgroups(D, 16 * NT);
   // a sequence's fixed cost in chunk units of one workgroup's streaming
-  // time: twice as many wavefronts stream a chunk in half the time
-  k.seg_cost = kSkSegCost * NW / 4;
+  // time (at D = 64 twice as many wavefronts would stream a chunk in half
+  // the time; at D = 128 the measured optimum of the shape)
+  k.seg_cost = D == 128 ? kSkSegCost128(NW) : kSkSegCost * NW / 4;
   if (a.kv8)
     hipLaunchKernelGGL((decode_sk_kernel<T, D, NT, PF, HALVES, true, NW>), dim3(k.n_wg),
                        dim3(kBlock), 0, stream, a, k);
@@ -628,7 +629,7 @@ int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
   // <T, D, NT, PF, HALVES, NW>: the D = 128 variants have room for one
   // chunk in flight per wavefront, the D = 64 ones for two. At D = 128 a
   // batch of decode sequences alone runs 4-wavefront workgroups, one per CU
-  // (cfg5: 33.8 against 34.7 us for 8 wavefronts); the decode part of a
+  // (cfg5: 32.9 against 34.7 us for 8 wavefronts); the decode part of a
   // mixed batch (qfilter 1) 8-wavefront ones, as in the one-launch mixed
   // kernel.
   const bool mixed = a.qfilter == 1;

@@ -140,10 +140,11 @@ struct AttnArgs {
   float* ws_o;       // [units][ROWS][d] unnormalised partial outputs
   float* ws_ml;      // [units][ROWS][2] (running max (log2 units), sum)
   int* status;
-  // fused append (partition decode kernel and MFMA prefill kernel; all null
-  // otherwise): the K/V rows of sequence s's query tokens go to positions
-  // new_pos[s], new_pos[s] + 1, ... of its table, and the attention uses
-  // them from k_new / v_new
+  // fused append (partition decode kernel, MFMA prefill kernel and the
+  // decode shares of the one-launch mixed kernel; all null otherwise): the
+  // K/V rows of sequence s's query tokens go to positions new_pos[s],
+  // new_pos[s] + 1, ... of its table, and the attention uses them from
+  // k_new / v_new
   const void* k_new;
   const void* v_new;
   const int32_t* new_pos;
@@ -176,8 +177,13 @@ constexpr int kSkMaxWg = 512;  // workgroups of the persistent kernel, at most
 // A sequence's fixed cost in the persistent kernel (Q load, table slice,
 // wavefront merge, output or partial write) measured in 32-token chunks of
 // a 4-wavefront workgroup's streaming time (scaled by the launch to its
-// workgroup size).
+// workgroup size). At head dim 128 the launch uses the measured optimum of
+// its workgroup shape instead (kSkSegCost128).
 constexpr int kSkSegCost = 5;
+// At head dim 128, one workgroup per CU: 4 wavefronts 9 (config 5: 3 / 5 /
+// 7 / 9 / 11 / 13 / 16 gave 35.7 / 33.8 / 33.0 / 32.9 / 33.2 / 33.6 / 34.2
+// us), 8 wavefronts 10 (8, 12, 14 and 20 slower).
+constexpr int kSkSegCost128(int waves) { return waves == 4 ? 9 : 10; }
 // Context bound from which part_tokens = 0 selects the persistent kernel.
 constexpr int kSkAutoKv = 4096;
 
