@@ -320,12 +320,15 @@ template <typename T, bool HALVES>
 int launch_t(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
   const dim3 grid(a.n_seq * a.hkv, p.parts_max);
   const int nt = a.group / 16;
-  // the D = 128 variants have room for one chunk in flight per wavefront,
-  // the D = 64 ones for two
+  // one chunk in flight per wavefront: at D = 128 the register budget
+  // allows no more; at D = 64 it measured fastest (cfg4: 12.8 against 13.4
+  // us for two and 14.1 / 14.2 us for three / four; the whole grid is
+  // resident at once, and fewer registers leave room for more wavefronts
+  // per SIMD)
   if (a.d == 64 && nt == 1)
-    launch_v<T, 64, 1, 2, HALVES>(a, grid, stream);
+    launch_v<T, 64, 1, 1, HALVES>(a, grid, stream);
   else if (a.d == 64 && nt == 2)
-    launch_v<T, 64, 2, 2, HALVES>(a, grid, stream);
+    launch_v<T, 64, 2, 1, HALVES>(a, grid, stream);
   else if (a.d == 128 && nt == 1)
     launch_v<T, 128, 1, 1, HALVES>(a, grid, stream);
   else if (a.d == 128 && nt == 2)
