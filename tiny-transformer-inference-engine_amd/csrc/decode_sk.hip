@@ -626,15 +626,16 @@ int launch_v(const AttnArgs& a, SkArgs k, hipStream_t stream) {
 template <typename T, bool HALVES>
 int launch_t(const AttnArgs& a, const SkArgs& k, hipStream_t stream) {
   const int nt = a.group / 16;
-  // <T, D, NT, PF, HALVES, NW>: the D = 128 variants have room for one
-  // chunk in flight per wavefront, the D = 64 ones for two. At D = 128 a
+  // <T, D, NT, PF, HALVES, NW>: one chunk in flight per wavefront (at
+  // D = 128 the register budget allows no more; at D = 64 it measured faster
+  // than two: cfg4 forced onto this kernel 15.5 against 16.1 us). At D = 128 a
   // batch of decode sequences alone runs 4-wavefront workgroups, one per CU
   // (cfg5: 32.9 against 34.7 us for 8 wavefronts); the decode part of a
   // mixed batch (qfilter 1) 8-wavefront ones, as in the one-launch mixed
   // kernel.
   const bool mixed = a.qfilter == 1;
-  if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 2, HALVES, 4>(a, k, stream);
-  if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 2, HALVES, 4>(a, k, stream);
+  if (a.d == 64 && nt == 1) return launch_v<T, 64, 1, 1, HALVES, 4>(a, k, stream);
+  if (a.d == 64 && nt == 2) return launch_v<T, 64, 2, 1, HALVES, 4>(a, k, stream);
   if (a.d == 128 && nt == 1)
     return mixed ? launch_v<T, 128, 1, 1, HALVES, 8>(a, k, stream)
                  : launch_v<T, 128, 1, 1, HALVES, 4>(a, k, stream);
