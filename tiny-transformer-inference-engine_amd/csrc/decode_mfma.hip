@@ -66,13 +66,25 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   const int tspec = table[max(0, min(spec_blk0 + (int)threadIdx.x, a.max_blk - 1))];
   v8 qf[NT][D / 32];
   if (s < a.n_tokens) load_q<T, D, NT>(qf, q, (int64_t)s * a.hq + kvh * G, grp, l16);
+  // fused append: the new row's position and its pieces are requested with
+  // Q (the pieces of query token s, again once query_start_loc has arrived
+  // if it is not s), so the append adds no round trip ahead of the chunks
+  int new_pos_s = -1;
+  u32x4 new_piece{};
+  if constexpr (APP) {
+    new_pos_s = a.new_pos[s];
+    if (s < a.n_tokens) new_piece = load_new_row<D>(a, s, kvh, threadIdx.x);
+  }
   TileGeom g;
   if (!tile_geom(a, s, 0, G, g)) return;
   if (part >= g.nparts) return;
   const int kv_lo = part * g.part_len;
   const int kv_hi = min(kv_lo + g.part_len, g.kv_limit);
   const int64_t qrow0 = (int64_t)g.q_begin * a.hq + kvh * G;
-  if (g.q_begin != s) load_q<T, D, NT>(qf, q, qrow0, grp, l16);  // uniform
+  if (g.q_begin != s) {  // uniform
+    load_q<T, D, NT>(qf, q, qrow0, grp, l16);
+    if constexpr (APP) new_piece = load_new_row<D>(a, g.q_begin, kvh, threadIdx.x);
+  }
   // the speculative window is this partition's first one unless the
   // sequence outgrew the planned bound (longer partitions)
   const bool spec_ok = g.part_len == a.part_tokens;
@@ -105,7 +117,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   int new_pos = -1;
   bool new_write = false, new_pending = false;  // pending: row buffer still to fill
   if constexpr (APP) {
-    new_pos = a.new_pos[s];
+    new_pos = new_pos_s;
     const bool new_here = new_pos >= kv_lo && new_pos < kv_hi;
     new_write = part == g.nparts - 1;
     if (new_here) nr.pos = new_pos;
@@ -125,8 +137,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     __syncthreads();  // previous window's table no longer read
     const bool spec = spec_ok && lo == kv_lo;
     if (APP && new_pending) {
-      // the new row's load is in flight with the table slice's
-      const u32x4 piece = load_new_row<D>(a, g.q_begin, kvh, threadIdx.x);
+      const u32x4 piece = new_piece;
       if (spec) {
         if ((int)threadIdx.x < nblk) tbl[threadIdx.x] = tspec;
       } else {
@@ -146,8 +157,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   }
   if (bad_block && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
   if (APP && new_write) {
-    if (new_pending) put_new_row<D>(new_lds, load_new_row<D>(a, g.q_begin, kvh, threadIdx.x),
-                                    threadIdx.x);
+    if (new_pending) put_new_row<D>(new_lds, new_piece, threadIdx.x);
     // each thread stores the piece it put into the buffer itself
     store_new_row<T, D, KV8>(new_lds, a, s, kvh, new_pos, tbl, last_blk_lo, last_nblk,
                              threadIdx.x);
