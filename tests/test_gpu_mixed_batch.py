@@ -175,3 +175,27 @@ def test_mixed_call_without_prefill_rows_still_appends(bound):
     torch.cuda.synchronize()
     assert torch.equal(pool_a.kv, pool_b.kv), "pools differ"
     assert torch.equal(out_a, out_b), "outputs differ"
+
+
+# The one-launch form at its edges: no decode sequence at all (the decode
+# workgroups find nothing to do), a single one, and a single prefill
+# sequence beside many decodes.
+@pytest.mark.parametrize("n_dec,chunks", [
+    (0, [(0, 128), (300, 64)]),
+    (1, [(0, 128), (0, 200)]),
+    (130, [(50, 40)]),
+], ids=["prefill-only", "one-decode", "one-prefill"])
+def test_mixed_one_launch_edges(n_dec, chunks):
+    print(f"[mixed one launch edges] n_dec={n_dec} chunks={chunks}", flush=True)
+    pool_a, meta, q, k, v = mixed_batch(n_dec, chunks, 32, 128, torch.bfloat16, 16, seed=35)
+    meta.max_kv_len = 8192  # the persistent decode kernel
+    pool_b = KVPool(1, 16, pool_a.num_blocks, 1, 128, torch.bfloat16, torch.device(DEV))
+    pool_b.kv.copy_(pool_a.kv)
+    pool_a.write_from_table(0, k, v, meta)
+    out_a = paged_attention_meta(q, pool_a.kv[0, 0], pool_a.kv[0, 1], meta)
+    out_b = paged_attention_append_meta(q, k, v, pool_b, 0, meta)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a.kv, pool_b.kv), "pools differ"
+    assert torch.equal(out_a, out_b), "outputs differ"
+    eo, _ = oracle(pool_a, meta, q)
+    assert np.abs(np64(out_b) - eo).max() <= 2e-2
