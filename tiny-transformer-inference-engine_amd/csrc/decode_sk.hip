@@ -548,10 +548,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void decode_sk_kernel(AttnArgs a, 
 // sequences (ad: qfilter 1, each new row taken from k_new), the rest the
 // prefill kernel's pair workgroups over the others, pair slot i % pre_slots
 // of kv head i / pre_slots (ap: qfilter 2, with the fused append of every
-// row of the batch). No workgroup reads what another writes in this launch:
-// the decode shares never read their new rows' pool slots' contents (they
-// are overwritten in LDS), and the prefill pairs read their own new rows from
-// k_new / v_new. Dispatched in order, the decode shares fill the CUs first,
+// row of the batch). No workgroup uses what another writes in this launch:
+// a decode share loads its new row's pool slot with the rest of the chunk
+// (a prefill workgroup may be writing it at that moment) but replaces it in
+// LDS with the row from k_new / v_new before any use, and the prefill pairs
+// read their own new rows from k_new / v_new. Dispatched in order, the
+// decode shares fill the CUs first,
 // and each pair workgroup starts on a CU as soon as a share there has
 // ended, so the prefill's prologue and the decode shares' uneven ends
 // overlap instead of adding up across two launches. (Pair workgroups that
