@@ -199,3 +199,38 @@ def test_mixed_one_launch_edges(n_dec, chunks):
     assert torch.equal(out_a, out_b), "outputs differ"
     eo, _ = oracle(pool_a, meta, q)
     assert np.abs(np64(out_b) - eo).max() <= 2e-2
+
+
+def test_mixed_one_launch_graph_replays():
+    """The one-launch mixed call captured in a HIP graph (with a private
+    workspace): several replays, with eager calls of the same step in
+    between, each give the eager step's pool and output bit for bit."""
+    print("[mixed one launch graph]", flush=True)
+    pool, meta, q, k, v = mixed_batch(80, [(0, 128), (200, 96)], 32, 128, torch.bfloat16, 16,
+                                      seed=36)
+    meta.max_kv_len = 8192  # the persistent decode kernel: one launch
+    base = pool.kv.clone()
+    ref = paged_attention_append_meta(q, k, v, pool, 0, meta)
+    torch.cuda.synchronize()
+    ref_pool = pool.kv.clone()
+    ws = _native.Workspace()
+    out = torch.empty_like(q)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with _native.workspace_scope(ws), torch.cuda.stream(side):
+        paged_attention_append_meta(q, k, v, pool, 0, meta, out=out)  # warm-up
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with _native.workspace_scope(ws), torch.cuda.graph(g):
+        paged_attention_append_meta(q, k, v, pool, 0, meta, out=out)
+    for r in range(3):
+        pool.kv.copy_(base)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {r}: outputs differ"
+        assert torch.equal(pool.kv, ref_pool), f"replay {r}: pools differ"
+        eager = paged_attention_append_meta(q, k, v, pool, 0, meta)  # eager work between
+        torch.cuda.synchronize()
+        assert torch.equal(eager, ref)
