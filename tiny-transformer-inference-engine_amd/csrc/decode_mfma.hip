@@ -308,14 +308,18 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   if (cq == 0 && a.lse) a.lse[qrow] = L > 0.f ? (M + log2f(L)) * kLn2f : INFINITY;
 }
 
-// <T, D, NT, PF, OCC, HALVES, APP, KV8>: two wavefronts per SIMD
+// <T, D, NT, PF, OCC, HALVES, APP, KV8>: the register budget of two
+// wavefronts per SIMD at D = 128, four at D = 64 (the kernel needs about
+// 100 VGPRs there; the tighter target measured the 12-layer config-4 step
+// 156.4 against 157.6 us)
 template <typename T, int D, int NT, int PF, bool HALVES, bool KV8>
 void launch_k(const AttnArgs& a, dim3 grid, hipStream_t stream) {
+  constexpr int kOcc = D == 64 ? 4 : 2;
   if (a.new_pos)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, HALVES, true, KV8>), grid,
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, kOcc, HALVES, true, KV8>), grid,
                        dim3(kBlock), 0, stream, a);
   else
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, 2, HALVES, false, KV8>), grid,
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, NT, PF, kOcc, HALVES, false, KV8>), grid,
                        dim3(kBlock), 0, stream, a);
 }
 template <typename T, int D, int NT, int PF, bool HALVES>
