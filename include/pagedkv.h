@@ -87,12 +87,19 @@ extern "C" {
    fp8 pools: bf16/f16 Q, 16 or 32 query heads per kv head, d = 64 or 128. */
 #define PKV_KV_FP8 0x100
 
-/* part_tokens values of pkv_paged_attention selecting the persistent decode
+/* part_tokens values of pkv_paged_attention selecting a persistent decode
    kernel where it applies (bf16/f16, one query per sequence, 16 or 32
-   query heads per kv head, d = 64 or 128): PKV_PART_PERSISTENT, and
-   PKV_PART_STATIC, its name for its static equal shares (the same kernel). */
+   query heads per kv head, d = 64 or 128). Each gives every workgroup an
+   equal share of all sequences' chunks. PKV_PART_PERSISTENT and
+   PKV_PART_STATIC take the register-staged kernel (the automatic choice
+   for long context bounds); PKV_PART_STREAM takes the wavefront-specialised
+   kernel, whose producer wavefronts stream K/V into LDS by LDS-DMA while
+   consumer wavefronts compute, where it applies (a decode batch without the
+   fused append, 16-bit pools, d = 128, block size >= 16), else the
+   register-staged one. */
 #define PKV_PART_PERSISTENT (-1)
 #define PKV_PART_STATIC (-2)
+#define PKV_PART_STREAM (-3)
 
 #define PKV_OK 0
 #define PKV_ERR_INVALID (-1)     /* bad argument (shape, null pointer, ...) */
@@ -117,6 +124,10 @@ extern "C" {
                                           shared by overlapping calls); rows of
                                           sequences split across workgroups may
                                           be missing or wrong                 */
+#define PKV_STATUS_STALLED 512  /* attention (wavefront-specialised decode
+                                   kernel): a wait between its wavefronts ran
+                                   out of its poll bound and the kernel left
+                                   early; the outputs are not valid       */
 
 /* Library version (PKV_VERSION). */
 int pkv_version(void);

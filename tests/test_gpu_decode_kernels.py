@@ -1,8 +1,9 @@
 """The MFMA decode kernels (the split-K partition form, part_tokens > 0 or
-automatic below long context bounds; the persistent form with equal shares
-of all context chunks, part_tokens = PART_PERSISTENT or PART_STATIC)
-against the fp64 oracle, on the shapes that stress their
-work decomposition:
+automatic below long context bounds; the persistent forms with equal shares
+of all context chunks: register-staged, part_tokens = PART_PERSISTENT or
+PART_STATIC, and wavefront-specialised, PART_STREAM, which falls back to the
+register-staged one at head dim 64) against the fp64 oracle, on the shapes
+that stress their work decomposition:
 
   - one very long sequence, cut by every workgroup share (all partials,
     one last-arriving merger);
@@ -24,6 +25,7 @@ from serving.fake_paged_attn import paged_attn_fwd, paged_mqa_decode
 pytestmark = pytest.mark.gpu
 SK = _native.PART_PERSISTENT
 STATIC = _native.PART_STATIC
+STREAM = _native.PART_STREAM
 PART = 512  # the split-K partition kernel, 512-token partitions
 DEV = "cuda"
 SHAPES = [(16, 64), (32, 128), (16, 128), (32, 64)]  # (heads per kv head, D)
@@ -53,7 +55,7 @@ def check(out, lse, eo, el, what):
 
 
 @pytest.mark.parametrize("g,d", SHAPES)
-@pytest.mark.parametrize("part_tokens", [SK, STATIC, 0, 512])
+@pytest.mark.parametrize("part_tokens", [SK, STATIC, STREAM, 0, 512])
 def test_single_long_sequence(g, d, part_tokens):
     print(f"[decode long] g={g} d={d} part={part_tokens}", flush=True)
     p = workloads.decode_problem([30000], g, 1, d, 16, 2048, torch.bfloat16, DEV, seed=11)
@@ -76,8 +78,8 @@ def test_many_short_and_empty_sequences_repeated(g, d):
                                  DEV, seed=12)
     seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
     eo, el = oracle(p, seq_lens)
-    for rep in range(4):
-        pt = PART if rep % 2 == 0 else STATIC
+    for rep in range(6):
+        pt = (PART, STATIC, STREAM)[rep % 3]
         lse = torch.empty(len(lens), g, device=DEV)
         out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
                                part_tokens=pt)
@@ -101,7 +103,7 @@ def test_gqa_two_kv_heads_and_missing_queries(dtype):
     eo, el = ref.paged_attention(np64(q), np64(p.k_pool), np64(p.v_pool),
                                  p.block_tables.cpu().numpy(), p.seq_lens.cpu().numpy(),
                                  qsl.cpu().numpy())
-    for pt in (0, SK, STATIC, PART):
+    for pt in (0, SK, STATIC, STREAM, PART):
         O = torch.empty_like(q)
         L = torch.empty(T, g * hkv, device=DEV)
         paged_mqa_decode(q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, out=O, lse=L,
@@ -122,7 +124,7 @@ def test_cfg4_and_cfg5_kernels_agree():
         assert diff <= 2e-2, f"{name}: persistent vs partition kernel differ by {diff}"
     
 
-@pytest.mark.parametrize("pt", [SK, STATIC, PART])
+@pytest.mark.parametrize("pt", [SK, STATIC, STREAM, PART])
 def test_records_of_previous_call_do_not_leak(pt):
     """A call where every sequence is split across workgroups, then a call on
     the same workspace where some of those sequences have no query: rows are
@@ -153,14 +155,16 @@ def test_records_of_previous_call_do_not_leak(pt):
 
 def _counters():
     """The decode kernels' arrival counters in the library workspace on this
-    device: the partition kernel's (first 8 KiB) and the persistent kernel's
-    per-sequence ones (the last int of each 16-byte record after them)."""
+    device: the partition kernel's (first 8 KiB) and the persistent kernels'
+    per-sequence ones (the last int of each 16-byte record after them, and
+    the one before it, which the wavefront-specialised kernel uses for its
+    second head group)."""
     buf = _native.WORKSPACE._bufs[torch.cuda.current_device()]
     recs = buf[8 * 1024: 256 * 1024].view(torch.int32).view(-1, 4)
-    return torch.cat([buf[: 8 * 1024].view(torch.int32), recs[:, 3]])
+    return torch.cat([buf[: 8 * 1024].view(torch.int32), recs[:, 3], recs[:, 2]])
 
 
-@pytest.mark.parametrize("pt", [STATIC, PART])
+@pytest.mark.parametrize("pt", [STATIC, STREAM, PART])
 def test_cut_sequences_alternating_inputs_and_counters_reset(pt):
     """Pieces of long sequences are merged inside the kernel by the last
     workgroup to arrive, from partials other workgroups (on other XCDs)
@@ -208,8 +212,8 @@ def test_persistent_random_length_mixes(seed):
                                  seed=200 + seed)
     seq_lens = torch.as_tensor(lens, dtype=torch.int32, device=DEV)
     eo, el = oracle(p, seq_lens)
-    for rep in range(4):
-        pt = PART if rep % 2 == 0 else STATIC
+    for rep in range(6):
+        pt = (PART, STATIC, STREAM)[rep % 3]
         lse = torch.empty(n, g, device=DEV)
         out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, seq_lens, lse=lse,
                                part_tokens=pt)
@@ -218,7 +222,7 @@ def test_persistent_random_length_mixes(seed):
         assert int(_counters().abs().sum()) == 0, "arrival counters not reset"
 
 
-@pytest.mark.parametrize("pt", [STATIC, 512])
+@pytest.mark.parametrize("pt", [STATIC, STREAM, 512])
 def test_in_kernel_merges_replayed_from_a_hip_graph(pt):
     """The decode launch with its in-kernel merges (arrival counters in the
     workspace, reset by the last contributor) captured in a HIP graph and

@@ -339,11 +339,12 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
   // leave the long sequences' workgroups running alone) take the persistent
   // kernel, which gives every workgroup the same share of the actual work
   const bool persistent = part_tokens == PKV_PART_PERSISTENT ||
-                          part_tokens == PKV_PART_STATIC ||
+                          part_tokens == PKV_PART_STATIC || part_tokens == PKV_PART_STREAM ||
                           (part_tokens == 0 && kv_bound >= kSkAutoKv);
   if (mfma && persistent && sk_fits(virt, max_blk)) {
     // persistent kernel: partials of at most two segments per workgroup
     p.kind = 2;
+    p.ws = part_tokens == PKV_PART_STREAM;
     p.rows = group;
     p.tiles_max = 1;
     p.part_tokens = 0;
@@ -462,7 +463,11 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
   if (p.parts_max > 65535 || p.tiles_max > 65535)
     return fail(PKV_ERR_UNSUPPORTED, "attention grid too large (%d parts, %d tiles, %d seq*hkv)",
                 p.parts_max, p.tiles_max, a.n_seq * a.hkv);
-  if (p.kind == 2) return launch_decode_sk(a, sk_args_for(a), dtype, stream);
+  if (p.kind == 2) {
+    if (p.ws && decode_ws_supported(a, dtype))
+      return launch_decode_ws(a, sk_args_for(a), dtype, stream);
+    return launch_decode_sk(a, sk_args_for(a), dtype, stream);
+  }
   if (p.kind == 1) {
     if (dtype == PKV_DTYPE_BF16) return launch_mfma<bf16>(a, p, dtype, stream);
     return launch_mfma<f16>(a, p, dtype, stream);

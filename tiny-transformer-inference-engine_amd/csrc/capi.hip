@@ -136,7 +136,7 @@ size_t pkv_attention_workspace_bytes(int n_seq, int max_q_len, int hq, int hkv,
                                      int max_kv_len, int part_tokens,
                                      int dtype) {
   if (n_seq <= 0 || max_q_len <= 0 || hkv <= 0 || hq <= 0 || hq % hkv != 0 ||
-      part_tokens < PKV_PART_STATIC)
+      part_tokens < PKV_PART_STREAM)
     return 0;
   // query_start_loc is required whenever max_q_len > 1
   return plan_split(n_seq, max_q_len, hq, hkv, d, max_blk, block_size, max_kv_len,
@@ -174,9 +174,9 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
     return fail(PKV_ERR_INVALID, "blocksize %d must be a power of two", block_size);
   if (n_seq < 0 || max_blk < 0 || num_blocks < 0 || max_q_len < 0 || n_tokens < 0)
     return fail(PKV_ERR_INVALID, "bad sizes");
-  if (part_tokens < PKV_PART_STATIC)
-    return fail(PKV_ERR_INVALID, "part_tokens %d: the negative values are PKV_PART_PERSISTENT "
-                "and PKV_PART_STATIC", part_tokens);
+  if (part_tokens < PKV_PART_STREAM)
+    return fail(PKV_ERR_INVALID, "part_tokens %d: the negative values are PKV_PART_PERSISTENT, "
+                "PKV_PART_STATIC and PKV_PART_STREAM", part_tokens);
   if (!query_start_loc && n_tokens != n_seq)
     return fail(PKV_ERR_INVALID, "without query_start_loc, n_tokens (%d) must equal n_seq (%d)",
                 n_tokens, n_seq);
@@ -362,7 +362,7 @@ int pkv_paged_attention_noalloc(void* out, float* lse, const void* q, const void
                                 int dtype, int* status, void* stream) {
   g_err[0] = 0;
   if (n_seq > 0 && max_q_len > 0 && hkv > 0 && hq > 0 && hq % hkv == 0 &&
-      part_tokens >= PKV_PART_STATIC) {
+      part_tokens >= PKV_PART_STREAM) {
     const size_t need = plan_split(n_seq, max_q_len, hq, hkv, d, max_blk, block_size,
                                    max_kv_len, part_tokens, dtype, query_start_loc != nullptr)
                             .ws_bytes;

@@ -186,6 +186,9 @@ constexpr int kSkSegCost = 5;
 constexpr int kSkSegCost128(int waves) { return waves == 4 ? 9 : 10; }
 // Context bound from which part_tokens = 0 selects the persistent kernel.
 constexpr int kSkAutoKv = 4096;
+// A sequence's fixed cost in the wavefront-specialised persistent kernel
+// (decode_ws.hip), in 32-token chunks of a workgroup's streaming time.
+constexpr int kWsSegCost = 4;
 
 struct SkArgs {
   int n_wg;         // workgroups launched
@@ -204,6 +207,7 @@ inline size_t sk_workspace_bytes(int group, int d) {
 struct AttnPlan {
   int kind;        // 0 = generic rows kernel, 1 = MFMA partition kernel,
                    // 2 = MFMA persistent kernel, 3 = MFMA prefill kernel
+  bool ws;         // kind 2: the wavefront-specialised form where it applies
   int rows;        // rows per tile of the chosen kernel
   int part_tokens;
   int parts_max;
@@ -333,6 +337,14 @@ int launch_decode_sk(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t 
 bool mixed_sk_supported(const AttnArgs& ap, int dtype);
 int launch_mixed_sk(const AttnArgs& ad, const SkArgs& k, const AttnArgs& ap, int dtype,
                     hipStream_t stream);
+// Wavefront-specialised persistent decode kernel (decode_ws.hip): producer
+// wavefronts stream K/V into an LDS ring by LDS-DMA, consumer wavefronts
+// compute. Decode batches (qfilter 0, no fused append) with bf16/fp16
+// queries and 16-bit pools, head dim 128, 16 or 32 query heads per kv head,
+// block size >= 16.
+int ws_workgroups();
+bool decode_ws_supported(const AttnArgs& a, int dtype);
+int launch_decode_ws(const AttnArgs& a, const SkArgs& k, int dtype, hipStream_t stream);
 // The persistent kernel's arguments for launch view a (workspace layout:
 // arrival records after the counter header, then the partials).
 SkArgs sk_args_for(const AttnArgs& a);

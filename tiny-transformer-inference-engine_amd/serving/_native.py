@@ -36,12 +36,16 @@ PKV_STATUS_NONFINITE = 32
 PKV_STATUS_BAD_DISTRIBUTION = 64
 PKV_STATUS_SAMPLE_OVERFLOW = 128
 PKV_STATUS_DIRTY_WORKSPACE = 256
-# part_tokens values selecting a persistent decode kernel: the one the
-# library prefers, the one with static equal shares, or the dynamically
-# scheduled one (largest-first work items drawn from a counter; up to 1024
-# sequence x kv head pairs and block_size >= 16, else the static one)
+PKV_STATUS_STALLED = 512
+# part_tokens values selecting a persistent decode kernel (every workgroup an
+# equal share of all sequences' chunks): PART_PERSISTENT and PART_STATIC the
+# register-staged kernel (also the automatic choice for long context
+# bounds), PART_STREAM the wavefront-specialised one (producer wavefronts
+# streaming K/V into LDS by LDS-DMA, consumer wavefronts computing) where it
+# applies, else the register-staged one
 PART_PERSISTENT = -1
 PART_STATIC = -2
+PART_STREAM = -3
 
 _lib = None
 _lock = threading.Lock()
