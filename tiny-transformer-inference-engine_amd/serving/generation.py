@@ -1,12 +1,22 @@
 """Paged generation loops — drop-in for serving/generation.py.
 
-generate_batched (greedy, reference generation.py:112-148): one prefill step
-for all prompts, then max_new_tokens-1 decode steps of one token per
-sequence; blocks are released in a finally block. generate_paged /
-prefill_seq / decode_step are the single-sequence variants (:71-110).
-generate_batched_text (:11-69) additionally needs a tokenizer; the
-reference's tiktoken "gpt2" encoding is used when importable, otherwise pass
-`tokenizer` (any object with encode_ordinary).
+Entry points and their reference counterparts:
+  generate_batched      serving/generation.py:112-148  greedy, token ids in
+  generate_batched_text serving/generation.py:11-69    sampled, text in,
+                                                       stops a row at EOS
+  generate_paged        serving/generation.py:91-110   greedy, one sequence
+  prefill_seq           serving/generation.py:71-77
+  decode_step           serving/generation.py:80-88
+
+The batched entry points share one driver (_drive): a _Cohort holds the
+calls' sequences, feeds the model one prefill step of whole prompts and then
+at most max_new_tokens - 1 decode steps of one token per running sequence,
+and returns every block to the allocator when the call ends, normally or by
+an exception. Per step the next tokens of the whole batch come from one
+device call (one argmax kernel, or one sampling kernel) and one
+device-to-host copy, instead of one per row. A row that samples
+eos_token_id stops there; the EOS token is not part of its output, and the
+decode steps after it leave that row out of the batch.
 """
 from __future__ import annotations
 
@@ -17,80 +27,89 @@ from .sampling import greedy, sample
 from .sequence import Sequence
 
 
-def _argmax_tokens(logits):
-    # one argmax launch and one device->host copy per step for the whole batch
+class _Cohort:
+    """The sequences of one batched call.
+
+    rows      Sequence objects, in prompt order
+    produced  tokens emitted per row so far
+    running   indices of the rows still generating, ascending (the row order
+              of the next decode batch)
+    feed      the token each running row feeds to the next decode step
+    """
+
+    def __init__(self, id_lists, block_size, alloc, device):
+        self.alloc = alloc
+        self.device = device
+        self.rows = [Sequence(n, list(ids), block_size) for n, ids in enumerate(id_lists)]
+        self.produced = [[] for _ in self.rows]
+        self.running = list(range(len(self.rows)))
+        self.feed = {}
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        for row in self.rows:
+            row.release(self.alloc)
+        return False
+
+    def prefill_batch(self):
+        for row in self.rows:
+            row.ensure_blocks(self.alloc)
+        return build_batch_step([(row, row.token_ids) for row in self.rows], self.device)
+
+    def decode_batch(self):
+        entries = []
+        for n in self.running:
+            row = self.rows[n]
+            row.append_token(self.feed[n])
+            row.ensure_blocks(self.alloc)
+            entries.append((row, [self.feed[n]]))
+        return build_batch_step(entries, self.device)
+
+    def accept(self, tokens, stop_id):
+        """tokens[i] is the pick of batch row i, i.e. of rows[running[i]]."""
+        still = []
+        for n, tok in zip(self.running, tokens):
+            if stop_id is not None and tok == stop_id:
+                continue
+            self.produced[n].append(tok)
+            self.feed[n] = tok
+            still.append(n)
+        self.running = still
+
+
+def _drive(model, pool, cohort, max_new_tokens, pick, stop_id=None):
+    cohort.accept(pick(model.forward_batch(cohort.prefill_batch(), pool)), stop_id)
+    for _ in range(max_new_tokens - 1):
+        if not cohort.running:
+            break
+        cohort.accept(pick(model.forward_batch(cohort.decode_batch(), pool)), stop_id)
+    return cohort.produced
+
+
+def _model_device(model):
+    return next(model.parameters()).device
+
+
+def _greedy_ids(logits):
     return greedy(logits)[:, 0].tolist()
 
 
 @torch.no_grad()
 def generate_batched(model, prompts_ids, max_new_tokens, pool, alloc, block_size=16):
-    """prompts_ids: list of token-id lists. Returns the greedy continuation
-    of each, in order."""
+    """prompts_ids: list of token-id lists. Returns the greedy continuation of
+    each (max_new_tokens tokens, no EOS stop), in prompt order."""
     if max_new_tokens < 0:
         raise ValueError("max_new_tokens must be >= 0")
     if not prompts_ids:
         return []
-    if any(not prompt for prompt in prompts_ids):
+    if not all(prompts_ids):
         raise ValueError("every prompt must contain at least one token")
     if max_new_tokens == 0:
         return [[] for _ in prompts_ids]
-    device = next(model.parameters()).device
-    seqs = [Sequence(i, list(p), block_size) for i, p in enumerate(prompts_ids)]
-    outputs = [[] for _ in seqs]
-    try:
-        for s in seqs:
-            s.ensure_blocks(alloc)
-        batch = build_batch_step([(s, s.token_ids) for s in seqs], device)
-        next_tokens = _argmax_tokens(model.forward_batch(batch, pool))
-        for out, t in zip(outputs, next_tokens):
-            out.append(t)
-        for _ in range(max_new_tokens - 1):
-            for s, t in zip(seqs, next_tokens):
-                s.append_token(t)
-                s.ensure_blocks(alloc)
-            batch = build_batch_step([(s, [t]) for s, t in zip(seqs, next_tokens)], device)
-            next_tokens = _argmax_tokens(model.forward_batch(batch, pool))
-            for out, t in zip(outputs, next_tokens):
-                out.append(t)
-        return outputs
-    finally:
-        for s in seqs:
-            s.release(alloc)
-
-
-@torch.no_grad()
-def prefill_seq(model, seq, pool, alloc):
-    seq.ensure_blocks(alloc)
-    device = next(model.parameters()).device
-    ids = torch.tensor([seq.token_ids], dtype=torch.long, device=device)
-    return int(model(ids, pool, seq.block_table, start=0)[0, -1].argmax())
-
-
-@torch.no_grad()
-def decode_step(model, seq, pool, alloc, token_id):
-    seq.append_token(token_id)
-    seq.ensure_blocks(alloc)
-    device = next(model.parameters()).device
-    x = torch.tensor([[token_id]], dtype=torch.long, device=device)
-    return int(model(x, pool, seq.block_table, start=seq.num_tokens - 1)[0, -1].argmax())
-
-
-@torch.no_grad()
-def generate_paged(model, prompt_ids, max_new_tokens, pool, alloc, block_size=16):
-    if max_new_tokens < 0:
-        raise ValueError("max_new_tokens must be >= 0")
-    if not prompt_ids:
-        raise ValueError("prompt must contain at least one token")
-    if max_new_tokens == 0:
-        return []
-    seq = Sequence(0, list(prompt_ids), block_size)
-    try:
-        out = [prefill_seq(model, seq, pool, alloc)]
-        while len(out) < max_new_tokens:
-            out.append(decode_step(model, seq, pool, alloc, out[-1]))
-        return out
-    finally:
-        seq.release(alloc)
+    with _Cohort(prompts_ids, block_size, alloc, _model_device(model)) as cohort:
+        return _drive(model, pool, cohort, max_new_tokens, _greedy_ids)
 
 
 def _default_tokenizer():
@@ -106,8 +125,10 @@ def _default_tokenizer():
 def generate_batched_text(model, cfg, prompts, max_new_tokens, eos_token_id,
                           pool, alloc, temperature=1.0, top_k=32, top_p=0.9,
                           block_size=16, tokenizer=None):
-    """Sampled batched generation from text prompts (reference
-    generation.py:11-69): stops a sequence at eos_token_id."""
+    """Sampled batched generation from text prompts. Returns the token ids
+    each prompt produced before it sampled eos_token_id (or before
+    max_new_tokens). tokenizer: any object with encode_ordinary(str); the
+    reference's tiktoken "gpt2" encoding when None."""
     if max_new_tokens < 0:
         raise ValueError("max_new_tokens must be >= 0")
     if not prompts:
@@ -115,49 +136,60 @@ def generate_batched_text(model, cfg, prompts, max_new_tokens, eos_token_id,
     if temperature <= 0 or top_k < 0 or not 0 < top_p <= 1:
         raise ValueError("invalid sampling parameters")
     enc = tokenizer if tokenizer is not None else _default_tokenizer()
-    device = next(model.parameters()).device
-    prompt_ids = [enc.encode_ordinary(p) for p in prompts]
-    if any(not ids for ids in prompt_ids):
+    id_lists = [enc.encode_ordinary(text) for text in prompts]
+    if not all(id_lists):
         raise ValueError("every prompt must encode to at least one token")
-    if any(len(ids) + max_new_tokens > cfg.max_seq_len for ids in prompt_ids):
+    if max(len(ids) for ids in id_lists) + max_new_tokens > cfg.max_seq_len:
         raise ValueError("prompt plus requested generation exceeds max_seq_len")
     if max_new_tokens == 0:
         return [[] for _ in prompts]
 
-    seqs = [Sequence(i, list(ids), block_size) for i, ids in enumerate(prompt_ids)]
-    outputs = [[] for _ in seqs]
+    def pick(logits):
+        return sample(logits, temperature=temperature, top_k=top_k, top_p=top_p)[:, 0].tolist()
 
-    def pick(row):
-        return int(sample(row.unsqueeze(0), temperature=temperature,
-                          top_k=top_k, top_p=top_p).item())
+    with _Cohort(id_lists, block_size, alloc, _model_device(model)) as cohort:
+        return _drive(model, pool, cohort, max_new_tokens, pick, stop_id=eos_token_id)
+
+
+def _last_position_argmax(model, seq, pool, new_ids):
+    """Runs new_ids (the last len(new_ids) tokens of seq) through the
+    single-sequence model call and returns the argmax at the last position."""
+    x = torch.tensor([new_ids], dtype=torch.long, device=_model_device(model))
+    logits = model(x, pool, seq.block_table, start=seq.num_tokens - len(new_ids))
+    return int(logits[0, -1].argmax())
+
+
+@torch.no_grad()
+def prefill_seq(model, seq, pool, alloc):
+    """Whole prompt of seq from position 0; returns its greedy next token."""
+    seq.ensure_blocks(alloc)
+    return _last_position_argmax(model, seq, pool, seq.token_ids)
+
+
+@torch.no_grad()
+def decode_step(model, seq, pool, alloc, token_id):
+    """Appends token_id to seq, runs it at its position, returns the greedy
+    next token."""
+    seq.append_token(token_id)
+    seq.ensure_blocks(alloc)
+    return _last_position_argmax(model, seq, pool, [token_id])
+
+
+@torch.no_grad()
+def generate_paged(model, prompt_ids, max_new_tokens, pool, alloc, block_size=16):
+    """Greedy single-sequence generation: one prefill call, then one decode
+    call per further token."""
+    if max_new_tokens < 0:
+        raise ValueError("max_new_tokens must be >= 0")
+    if not prompt_ids:
+        raise ValueError("prompt must contain at least one token")
+    if max_new_tokens == 0:
+        return []
+    seq = Sequence(0, list(prompt_ids), block_size)
     try:
-        for seq in seqs:
-            seq.ensure_blocks(alloc)
-        logits = model.forward_batch(build_batch_step([(s, s.token_ids) for s in seqs], device), pool)
-        next_tokens = {i: pick(logits[i]) for i in range(len(seqs))}
-        finished = [False] * len(seqs)
-        for i, token in next_tokens.items():
-            finished[i] = token == eos_token_id
-            if not finished[i]:
-                outputs[i].append(token)
-        for _ in range(max_new_tokens - 1):
-            if all(finished):
-                break
-            active = [i for i, done in enumerate(finished) if not done]
-            for i in active:
-                seqs[i].append_token(next_tokens[i])
-                seqs[i].ensure_blocks(alloc)
-            logits = model.forward_batch(
-                build_batch_step([(seqs[i], [next_tokens[i]]) for i in active], device), pool)
-            current = {}
-            for row, i in enumerate(active):
-                token = pick(logits[row])
-                current[i] = token
-                finished[i] = token == eos_token_id
-                if not finished[i]:
-                    outputs[i].append(token)
-            next_tokens = current
-        return outputs
+        out = [prefill_seq(model, seq, pool, alloc)]
+        while len(out) < max_new_tokens:
+            out.append(decode_step(model, seq, pool, alloc, out[-1]))
+        return out
     finally:
-        for seq in seqs:
-            seq.release(alloc)
+        seq.release(alloc)
