@@ -81,10 +81,11 @@ extern "C" {
 #define PKV_DTYPE_F16 1
 #define PKV_DTYPE_BF16 2
 /* Flag OR-ed into `dtype`: the K/V pools hold fp8 e4m3. Appends round each
-   new value to the nearest fp8 value (ties to even; magnitudes of 480 and
-   more, infinities and NaN give NaN), the bytes torch's conversion to
-   float8_e4m3fn gives; attention widens pool values exactly. Attention with
-   fp8 pools: bf16/f16 Q, 16 or 32 query heads per kv head, d = 64 or 128. */
+   new value to the nearest fp8 value (ties to even; magnitudes above 464,
+   those that round past 448, infinities and NaN give NaN), the bytes
+   torch's conversion to float8_e4m3fn gives; attention widens pool values
+   exactly. Attention with fp8 pools: bf16/f16 Q, 16 or 32 query heads per
+   kv head, d = 64 or 128. */
 #define PKV_KV_FP8 0x100
 
 /* part_tokens values of pkv_paged_attention selecting a persistent decode

@@ -189,8 +189,9 @@ def e4m3_codes(x) -> np.ndarray:
     index_put converts). Format: sign, 4 exponent bits (bias 7), 3 mantissa
     bits; no infinities; S.1111.111 is NaN; largest finite 1.75 * 2^8 = 448;
     below 2^-6 the values are the multiples of 2^-9. Rounding to nearest,
-    ties to even; a magnitude that rounds beyond 448 (>= 464), infinities
-    and NaN give NaN (0x7F with the sign)."""
+    ties to even; magnitudes above 464 (those that round past 448; 464
+    itself is a tie and goes to 448), infinities and NaN give NaN (0x7F with
+    the sign)."""
     x = np.asarray(x, dtype=np.float32)
     sign = (np.signbit(x).astype(np.uint8) << 7)
     with np.errstate(invalid="ignore"):  # signalling NaN inputs

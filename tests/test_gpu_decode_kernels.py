@@ -263,3 +263,29 @@ def test_in_kernel_merges_replayed_from_a_hip_graph(pt):
         torch.cuda.synchronize()
         assert torch.equal(out, eo) and torch.equal(lse, el), f"replay {k} differs"
         assert int(_counters().abs().sum()) == 0, f"replay {k}: counters not reset"
+
+
+@pytest.mark.parametrize("scale", [1e5, 1e-6])
+@pytest.mark.parametrize("g,d", [(32, 128), (16, 64)])
+@pytest.mark.parametrize("part_tokens", [SK, STATIC, STREAM, 0, 512])
+def test_bf16_value_range_through_staging_and_partials(scale, g, d, part_tokens):
+    """bf16 values far outside fp16's range (1e5: past fp16's largest finite
+    65504; 1e-6: among fp16's subnormals, a few bits of precision): the
+    wavefront staging and the split-K partials keep bf16's exponent range.
+    A long sequence cut by many shares, one of medium length, a short one.
+    Tolerance 2e-2 relative to the value scale."""
+    print(f"[decode bf16 range] scale={scale} g={g} d={d} part={part_tokens}", flush=True)
+    p = workloads.decode_problem([30000, 3000, 17], g, 1, d, 16, 4096, torch.bfloat16, DEV,
+                                 seed=17)
+    p.v_pool.mul_(scale)
+    lse = torch.empty(3, g, device=DEV)
+    out = paged_mqa_decode(p.q, p.k_pool, p.v_pool, p.block_tables, p.seq_lens, lse=lse,
+                           part_tokens=part_tokens)
+    torch.cuda.synchronize()
+    eo, el = oracle(p)
+    got = np64(out)
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - eo).max() / scale
+    assert err <= 2e-2, f"max err {err:.3e} x scale"
+    fin = np.isfinite(el)
+    np.testing.assert_allclose(lse.cpu().numpy()[fin], el[fin], rtol=0, atol=2e-2)

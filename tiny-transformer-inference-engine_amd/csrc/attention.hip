@@ -442,7 +442,7 @@ SkArgs sk_args_for(const AttnArgs& a) {
   k.seg_cost = kSkSegCost;
   char* ws = reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes;
   k.recs = reinterpret_cast<int4*>(ws + kWsCtrBytes);
-  k.part_o = reinterpret_cast<_Float16*>(a.ws_o);
+  k.part_o = reinterpret_cast<uint16_t*>(a.ws_o);
   k.part_ml = reinterpret_cast<float*>(k.part_o + (size_t)kSkMaxWg * 2 * a.group * a.d);
   return k;
 }

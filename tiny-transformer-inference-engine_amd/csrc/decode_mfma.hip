@@ -205,20 +205,14 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
     } else {
       const int64_t prow = unit * G + cb.head;
       if (a.merge_ctr) {
-        // O / sum rounded to fp16 (a weighted mean of value rows, so within
-        // their range: the reference computes in fp16 throughout,
-        // serving/fake_paged_attn.py:208-215) and the fp32 (max, sum):
-        // half the partial traffic of unnormalised fp32 rows. Written
-        // through to memory: the merging workgroup may sit on another XCD.
-        _Float16* po16 = reinterpret_cast<_Float16*>(a.ws_o) + prow * D;
+        // O / sum rounded to T (a weighted mean of value rows, so within
+        // their range; bf16 keeps fp32's exponent range) and the fp32
+        // (max, sum): half the partial traffic of unnormalised fp32 rows.
+        // Written through to memory: the merging workgroup may sit on
+        // another XCD.
+        uint16_t* po16 = reinterpret_cast<uint16_t*>(a.ws_o) + prow * D;
 #pragma unroll
-        for (int q = 0; q < Combine::NQ; ++q) {
-          const half4 h = half4{(_Float16)(cb.acc[q][0] * cb.inv), (_Float16)(cb.acc[q][1] * cb.inv),
-                                (_Float16)(cb.acc[q][2] * cb.inv), (_Float16)(cb.acc[q][3] * cb.inv)};
-          uint64_t b;
-          __builtin_memcpy(&b, &h, 8);
-          st_agent64(po16 + cb.col(q), b);
-        }
+        for (int q = 0; q < Combine::NQ; ++q) st_agent64(po16 + cb.col(q), pack4<T>(cb.acc[q], cb.inv));
         if (cb.cq == 0) {
           const float2 ml = make_float2(cb.M, cb.L);
           uint64_t bm;
@@ -268,17 +262,17 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
   floatx4 acc[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const _Float16* po16 = reinterpret_cast<const _Float16*>(a.ws_o);
+  const uint16_t* po16 = reinterpret_cast<const uint16_t*>(a.ws_o);
   for (int p0 = 0; p0 < g.nparts; p0 += kMB) {
     float2 ml[kMB];
-    half4 oo[kMB][NQ];
+    uint64_t oo[kMB][NQ];
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
       const int64_t row = (unit0 + min(p0 + j, g.nparts - 1)) * G + head;
       ml[j] = *reinterpret_cast<const float2*>(a.ws_ml + row * 2);
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
-        oo[j][q] = *reinterpret_cast<const half4*>(po16 + row * D + 4 * (cq + Combine::TPH * q));
+        oo[j][q] = *reinterpret_cast<const uint64_t*>(po16 + row * D + 4 * (cq + Combine::TPH * q));
     }
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
@@ -289,9 +283,7 @@ __global__ __launch_bounds__(kBlock, OCC) void decode_mfma_kernel(AttnArgs a) {
       L = L * sa + wl;
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
-        acc[q] = acc[q] * sa +
-                 floatx4{(float)oo[j][q][0], (float)oo[j][q][1], (float)oo[j][q][2],
-                         (float)oo[j][q][3]} * wl;
+        acc[q] = acc[q] * sa + unpack4<T>(oo[j][q]) * wl;
       M = Mn;
     }
   }

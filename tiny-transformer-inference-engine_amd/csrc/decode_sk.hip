@@ -153,11 +153,7 @@ __device__ __forceinline__ void merge_cut(const AttnArgs& a, const SkArgs& k, in
       const float wl = ml.y * exp2f(ml.x - Mn);  // this partial's weight
       L = L * sa + wl;
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        half4 oo;
-        __builtin_memcpy(&oo, &oor[j][q], 8);
-        acc[q] = acc[q] * sa + floatx4{(float)oo[0], (float)oo[1], (float)oo[2], (float)oo[3]} * wl;
-      }
+      for (int q = 0; q < NQ; ++q) acc[q] = acc[q] * sa + unpack4<T>(oor[j][q]) * wl;
       M = Mn;
     }
   }
@@ -182,8 +178,9 @@ struct SkGeo {
   static constexpr int kBlock = 64 * kWaves;
   static constexpr int G = 16 * NT;
   static constexpr int WAVE_BYTES = 2 * ChunkGeo<D>::BYTES;
-  using Combine = WaveCombine16<G, D, kWaves, kBlock>;
-  static constexpr int MERGE_BYTES = kWaves * G * Combine::OPITCH * 2;
+  template <typename S>
+  using Combine = WaveCombine16<S, G, D, kWaves, kBlock>;
+  static constexpr int MERGE_BYTES = kWaves * G * Combine<bf16>::OPITCH * 2;
   static constexpr int MAIN_BYTES = kWaves * WAVE_BYTES;
   // the wavefronts' chunk slices while streaming, the merge area after
   static constexpr int LDS_BYTES = MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES;
@@ -219,7 +216,7 @@ __device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
   constexpr int G = SG::G;
   constexpr int DT = D / 16;
   constexpr int WAVE_BYTES = SG::WAVE_BYTES;
-  using Combine = typename SG::Combine;
+  using Combine = typename SG::template Combine<T>;
   char* const lds = sm.lds;
   float(*const ml_lds)[G][2] = sm.ml_lds;
   int* const tbl = sm.tbl;
@@ -311,7 +308,7 @@ __device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
   bool bad_block = false;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   T* __restrict__ out = static_cast<T*>(a.out);
-  _Float16* ob = reinterpret_cast<_Float16*>(lds);
+  T* ob = reinterpret_cast<T*>(lds);
   // kTblCap - 1 blocks of tokens: a window that starts inside a block still
   // touches at most kTblCap table entries
   const int win = (kTblCap - 1) << a.bs_shift;
@@ -433,16 +430,14 @@ __device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
       st.l[nt] = head_lanes_sum(st.l[nt]);
     }
     __syncthreads();
-    // each wavefront's O / l in fp16 (see WaveCombine16)
+    // each wavefront's O / l rounded to T (see WaveCombine16)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const float il = st.l[nt] > 0.f ? 1.f / st.l[nt] : 0.f;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        *reinterpret_cast<half4*>(ob + (w * G + 16 * nt + l16) * Combine::OPITCH + 16 * dt +
-                                  4 * grp) =
-            half4{(_Float16)(st.o[nt][dt][0] * il), (_Float16)(st.o[nt][dt][1] * il),
-                  (_Float16)(st.o[nt][dt][2] * il), (_Float16)(st.o[nt][dt][3] * il)};
+        *reinterpret_cast<uint64_t*>(ob + (w * G + 16 * nt + l16) * Combine::OPITCH + 16 * dt +
+                                     4 * grp) = pack4<T>(st.o[nt][dt], il);
     }
     if (grp == 0) {
 #pragma unroll
@@ -471,17 +466,12 @@ __device__ __forceinline__ void decode_sk_body(AttnArgs a, SkArgs k, int wg,
           a.lse[qrow] = cb.L > 0.f ? (cb.M + log2f(cb.L)) * kLn2f : INFINITY;
       } else {
         // normalised by its own sum (a weighted mean of value rows, so its
-        // range is theirs) and rounded to fp16: half the partial traffic
+        // range is theirs) and rounded to T: half the partial traffic
         const int64_t prow = (int64_t)slot * G + cb.head;
 #pragma unroll
-        for (int q = 0; q < cb.NQ; ++q) {
-          const half4 h = half4{(_Float16)(cb.acc[q][0] * inv), (_Float16)(cb.acc[q][1] * inv),
-                                (_Float16)(cb.acc[q][2] * inv), (_Float16)(cb.acc[q][3] * inv)};
+        for (int q = 0; q < cb.NQ; ++q)
           // written through: the merging workgroup may sit on another XCD
-          uint64_t b;
-          __builtin_memcpy(&b, &h, 8);
-          st_agent64(k.part_o + prow * D + cb.col(q), b);
-        }
+          st_agent64(k.part_o + prow * D + cb.col(q), pack4<T>(cb.acc[q], inv));
         if (cb.cq == 0) {
           const float2 ml = make_float2(cb.M, cb.L);
           uint64_t b;

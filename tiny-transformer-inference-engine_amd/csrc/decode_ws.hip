@@ -228,21 +228,6 @@ __device__ __forceinline__ int ws_share_owner(int x, int C, int W) {
   return (int)(((int64_t)(x + 1) * W - 1) / C);
 }
 
-// 4 values of T packed into 8 bytes, and back
-template <typename T>
-__device__ __forceinline__ uint64_t pack4(floatx4 x, float s) {
-  T h[4] = {(T)(x[0] * s), (T)(x[1] * s), (T)(x[2] * s), (T)(x[3] * s)};
-  uint64_t b;
-  __builtin_memcpy(&b, h, 8);
-  return b;
-}
-template <typename T>
-__device__ __forceinline__ floatx4 unpack4(uint64_t b) {
-  T h[4];
-  __builtin_memcpy(h, &b, 8);
-  return floatx4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-}
-
 // Partial slot of contributor ww of a sequence cut over [w_first, w_last]
 // (decode_sk.hip's rule): its first segment's slot 2ww, except w_first's
 // when its share starts with an earlier sequence (2 w_first + 1).

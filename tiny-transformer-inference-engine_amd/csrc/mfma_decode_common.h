@@ -34,6 +34,23 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
+// 4 floats times s rounded to T and packed into 8 bytes, and back. Staging
+// and split-K partials use the kernel's element type: bf16 keeps fp32's
+// exponent range, fp16 holds any weighted mean of fp16 value rows.
+template <typename T>
+__device__ __forceinline__ uint64_t pack4(floatx4 x, float s) {
+  T h[4] = {(T)(x[0] * s), (T)(x[1] * s), (T)(x[2] * s), (T)(x[3] * s)};
+  uint64_t b;
+  __builtin_memcpy(&b, h, 8);
+  return b;
+}
+template <typename T>
+__device__ __forceinline__ floatx4 unpack4(uint64_t b) {
+  T h[4];
+  __builtin_memcpy(h, &b, 8);
+  return floatx4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
 template <typename T>
 struct Ops;
 template <>
@@ -612,15 +629,15 @@ struct WaveCombine {
 };
 
 // The same combination with the wavefront states staged as O / l rounded to
-// fp16 (half the LDS bytes of fp32 O; each is a weighted mean of value rows,
-// so within their range: the reference computes in fp16 throughout,
-// serving/fake_paged_attn.py:208-215): ob = [NW][G][OPITCH] halves, ml =
-// [NW][G] (m, l). Wavefront ww's weight is l_ww 2^(m_ww - M).
-template <int G, int D, int NW, int BLOCK>
+// the 16-bit element type S (half the LDS bytes of fp32 O; each is a
+// weighted mean of value rows, so within their range): ob = [NW][G][OPITCH]
+// values of S, ml = [NW][G] (m, l). Wavefront ww's weight is
+// l_ww 2^(m_ww - M).
+template <typename S, int G, int D, int NW, int BLOCK>
 struct WaveCombine16 {
   static constexpr int TPH = BLOCK / G;        // threads per head
   static constexpr int NQ = D / (4 * TPH);     // 4-column groups per thread
-  static constexpr int OPITCH = D + 8;         // halves
+  static constexpr int OPITCH = D + 8;         // values of S
   static_assert(BLOCK % G == 0 && NQ >= 1 && D % (4 * TPH) == 0, "block / head split");
   int head, cq;
   float M, L, inv;  // running max (base 2), sum, 1 / sum (0 when the sum is 0)
@@ -628,7 +645,7 @@ struct WaveCombine16 {
 
   __device__ __forceinline__ int col(int q) const { return 4 * (cq + TPH * q); }
 
-  __device__ __forceinline__ void run(const _Float16* ob, const float (*ml)[G][2], int tid) {
+  __device__ __forceinline__ void run(const S* ob, const float (*ml)[G][2], int tid) {
     head = tid / TPH;
     cq = tid - head * TPH;
     M = -INFINITY;
@@ -648,8 +665,8 @@ struct WaveCombine16 {
       for (int ww = 0; ww < NW; ++ww)
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-          const half4 h = *reinterpret_cast<const half4*>(ob + (ww * G + head) * OPITCH + col(q));
-          acc[q] += wt[ww] * floatx4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+          acc[q] += wt[ww] * unpack4<S>(
+                                 *reinterpret_cast<const uint64_t*>(ob + (ww * G + head) * OPITCH + col(q)));
         }
     }
     inv = L > 0.f ? 1.f / L : 0.f;

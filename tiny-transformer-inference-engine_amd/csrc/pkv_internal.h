@@ -30,8 +30,10 @@ inline int dtype_base(int dtype) { return dtype & ~PKV_KV_FP8; }
 
 // Nearest fp8 e4m3 value (OCP, torch.float8_e4m3fn: bias 7, 3 mantissa bits,
 // no infinities, S.1111.111 = NaN, largest finite 448) of x: ties to even;
-// |x| >= 480, infinities and NaN give NaN (0x7F with the sign bit); the
-// bytes torch's conversion gives. Values below 2^-6 are multiples of 2^-9.
+// magnitudes above 464 (those that round past 448: from 480 on by the first
+// test, between 464 and 480 by the rounding carry into S.1111.111),
+// infinities and NaN give NaN (0x7F with the sign bit); the bytes torch's
+// conversion gives. Values below 2^-6 are multiples of 2^-9.
 __device__ __forceinline__ unsigned f32_to_e4m3(float x) {
   unsigned b = __float_as_uint(x);
   const unsigned sign = (b >> 24) & 0x80u;
@@ -194,7 +196,8 @@ struct SkArgs {
   int n_wg;         // workgroups launched
   int seg_cost;     // overhead of one sequence in chunk units (share balance)
   int4* recs;       // [n_seq * hkv] per-pair records: .w is the arrival counter
-  _Float16* part_o; // [n_wg][2][G][D] partial outputs, normalised (O / sum)
+  uint16_t* part_o; // [n_wg][2][G][D] partial outputs, normalised (O / sum),
+                    // in the kernel's 16-bit element type
   float* part_ml;   // [n_wg][2][G][2] partial (max, sum)
 };
 
