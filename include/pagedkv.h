@@ -272,10 +272,13 @@ int pkv_paged_attention_append(void* out, float* lse, const void* q,
  * counters live in a 16 MiB scratch array the library holds on every device
  * it runs on, for the life of the process. A problem whose
  * pkv_attention_workspace_bytes() exceeds 16 MiB returns PKV_ERR_WORKSPACE.
- * The call allocates nothing (the first call on a device takes the array's
- * address and zeroes its counter header with a kernel on `stream`). All
- * calls on one device share that array: calls that overlap on one device
- * (different streams, or threads) race.
+ * The call allocates nothing. The array starts zero-filled (static storage
+ * of the library's code object) and every call leaves its counter header at
+ * zero; the first call on a device takes the array's address and zeroes that
+ * header once more with a fill kernel on `stream` (under graph capture that
+ * kernel becomes a node of the graph, run at every replay). All calls on one
+ * device share that array: calls that overlap on one device (different
+ * streams, or threads) race.
  */
 int pkv_paged_attention_noalloc(void* out, float* lse, const void* q,
                                 const void* k_pool, const void* v_pool,

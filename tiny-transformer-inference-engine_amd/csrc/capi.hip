@@ -305,9 +305,11 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
 }
 
 // Scratch of pkv_paged_attention_noalloc: one array per device, in the
-// library's code object (no allocation at call time). Its first
-// kWsCounterBytes are the counter header, which every call leaves at zero;
-// it is cleared once, when a device's address is first taken.
+// library's code object (no allocation at call time), zero-filled when the
+// code object is loaded. Its first kWsCounterBytes are the counter header,
+// which every call leaves at zero; a fill kernel clears it once more when a
+// device's address is first taken (a plain kernel, so the first call may be
+// under graph capture: the fill then runs at every replay of that graph).
 constexpr size_t kScratchBytes = size_t(16) << 20;
 static __device__ __align__(256) char scratch[kScratchBytes];
 
