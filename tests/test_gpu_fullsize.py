@@ -5,10 +5,12 @@ cfg4 decode step: the 12-layer, d_model 1024, vocab 50257 bf16 model at
 batch 128 (contexts U[256, 2048], block size 16) through forward_step.
 Every layer's library call (append + attention) is intercepted: the pool
 layer after it must equal the layer before it with the step's K/V rows
-written by oracle.paged_ref.append_from_table, bit for bit, and the
-attention output of 16 sampled sequences plus the shortest and the
-longest must match oracle.paged_ref.paged_attention (fp64) on the updated
-pool within 2e-2 absolute (bf16 storage, bf16 P in the PV product). The
+written by oracle.paged_ref.append_from_table, bit for bit; the attention
+output of all 128 sequences must match the reference's gather + SDPA path
+(oracle.torch_ref.paged_attention_sdpa, fp32) on the updated pool, and 16
+sampled sequences plus the shortest and the longest
+oracle.paged_ref.paged_attention (fp64), within 2e-2 absolute (bf16
+storage, bf16 P in the PV product). The
 same step is then captured as a HIP graph and replayed against eager steps:
 tokens, logits and pools bit-identical.
 
@@ -18,15 +20,17 @@ attending over a 512-token prompt chunk, one fused call, at block sizes 16
 and 32. Every pool slot no sequence owns holds 1e3 (the reference's
 tests/test.py garbage fill), so a key read past a context or through a
 wrong table entry shows. Pool rows bit-exact against the oracle's append;
-the 4 prefill sequences in full (causal, bottom-right aligned:
-pagedattn.cu:196-207) and 32 decode sequences against the oracle, outputs
-and lse within 2e-2.
+every row (256 decode rows and the 4 x 512 prefill rows, causal,
+bottom-right aligned: pagedattn.cu:196-207) against gather + SDPA in fp32;
+the 4 prefill sequences in full and 32 decode sequences against the fp64
+oracle, outputs and lse within 2e-2.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import paged_ref as ref
+from oracle import torch_ref
 from serving import workloads
 from serving.fake_paged_attn import paged_attention_append_meta
 from serving.graph_step import DecodeStepGraph
@@ -125,6 +129,14 @@ def test_cfg4_model_step_full_size_against_oracle_and_graph(monkeypatch):
         ek, ev = _expected_after_append(bk, bv, k, v, meta_, BS)
         assert np.array_equal(_bits(ak), ek), f"layer {layer}: K pool differs from the oracle append"
         assert np.array_equal(_bits(av), ev), f"layer {layer}: V pool differs from the oracle append"
+        # every sequence against gather + SDPA in fp32
+        nb_ = ak.shape[0] // BS
+        sdpa = torch_ref.paged_attention_sdpa(q.detach().cpu(), ak.view(nb_, BS, *ak.shape[1:]),
+                                              av.view(nb_, BS, *av.shape[1:]),
+                                              meta_.block_tables.cpu(), meta_.seq_lens.cpu(),
+                                              dtype=torch.float32)
+        _close(out.detach().float().cpu().numpy(), sdpa.numpy().astype(np.float64),
+               f"layer {layer} attention, all {N} rows vs SDPA")
         kp, vp, small = _compact(ak, av, tables, sample, BS)
         qs = q[sample].detach().float().cpu().numpy().astype(np.float64)
         sl = meta_.seq_lens.cpu().numpy()[sample]
@@ -190,6 +202,16 @@ def test_cfg5_mixed_step_full_size_against_oracle(bs):
     ek, ev = _expected_after_append(bk, bv, p.k, p.v, meta, bs)
     assert np.array_equal(_bits(ak), ek), "K pool differs from the oracle append"
     assert np.array_equal(_bits(av), ev), "V pool differs from the oracle append"
+
+    # every row (decode and prefill) against gather + SDPA in fp32
+    nb_ = ak.shape[0] // bs
+    sdpa = torch_ref.paged_attention_sdpa(p.q.cpu(), ak.view(nb_, bs, *ak.shape[1:]),
+                                          av.view(nb_, bs, *av.shape[1:]), meta.block_tables.cpu(),
+                                          meta.seq_lens.cpu(), meta.query_start_loc.cpu(),
+                                          dtype=torch.float32)
+    assert sdpa.shape == out.shape
+    _close(out.float().cpu().numpy(), sdpa.numpy().astype(np.float64),
+           f"bs {bs}: all {out.shape[0]} rows vs SDPA")
 
     n_dec = len(p.dec_lens)
     rng = np.random.default_rng(bs)
