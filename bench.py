@@ -692,8 +692,11 @@ def run_profile(args, torch):
         u = torch.rand(128, generator=g, device=dev)
         for _ in range(args.profile_iters):
             fused_ops.sample_rows(logits, 1.0, 32, 0.9, u)
+        ids = torch.empty(128, dtype=torch.long, device=dev)
+        for _ in range(args.profile_iters):
+            fused_ops.argmax_rows(logits, out=ids)
         torch.cuda.synchronize()
-        log(f"profile sampling: {args.profile_iters} launches")
+        log(f"profile sampling: {args.profile_iters} launches of sample_rows and of argmax_rows")
         return
     if args.profile == "cfg4":
         # the roofline's cold rotation: every layer's pool in turn

@@ -425,10 +425,16 @@ int pkv_linear_rope_qkv_rmsnorm(void* q_out, void* k_out, void* v_out, const voi
  * maximum, and a NaN counts as larger than any number (the first NaN
  * wins). Replaces logits.argmax as taken per sequence by the greedy loops
  * (serving/generation.py:77, :88, :132, :142) and greedy()
- * (sampling.py:5-137).
+ * (sampling.py:5-137). With a workspace of at least
+ * pkv_argmax_workspace_bytes(rows, vocab, dtype) bytes (256-byte aligned,
+ * zero-filled before its first use; every call leaves it zero-filled) a
+ * batch of fewer than 512 rows is split over several workgroups per row;
+ * without one (NULL), one workgroup per row. Same ids either way. Calls
+ * that overlap on one workspace race.
  */
 int pkv_argmax_rows(int64_t* ids, const void* logits, int64_t rows, int64_t vocab,
-                    int64_t row_stride, int dtype, void* stream);
+                    int64_t row_stride, int dtype, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /*
  * Sampling step of the scheduler (sampling.py:94-137, sample()): per row of
@@ -449,6 +455,13 @@ int pkv_argmax_rows(int64_t* ids, const void* logits, int64_t rows, int64_t voca
 int pkv_sample_rows(int64_t* ids, const void* logits, int64_t rows, int64_t vocab,
                     int64_t row_stride, float temperature, int top_k, float top_p,
                     const float* uniforms, int dtype, int* status, void* stream);
+
+/*
+ * Workspace bytes of pkv_argmax_rows for `rows` rows of `vocab` logits of
+ * `dtype` (no counterpart in the reference): per-row arrival counters and
+ * key words, one 128-byte line each; 0 when those rows are not split.
+ */
+size_t pkv_argmax_workspace_bytes(int64_t rows, int64_t vocab, int dtype);
 
 /*
  * Measurement helper, no counterpart in the reference: reads `bytes` bytes at

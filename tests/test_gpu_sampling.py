@@ -172,3 +172,57 @@ def test_sample_errors_and_overflow_fallback():
     for r in range(64):
         keep, _ = sref.sample_probs(y[r], 1.0, 32, 0.9)
         assert keep[tok[r]]
+
+
+# ---- split argmax rows (several workgroups per row, through the workspace)
+# against one workgroup per row (no workspace): the same ids
+
+
+def _abi_argmax(logits, ws):
+    rows, vocab = logits.shape
+    ids = torch.full((rows,), -7, dtype=torch.long, device=DEV)
+    wsb = 0 if ws is None else ws.numel()
+    rc = _native.lib().pkv_argmax_rows(ids.data_ptr(), logits.data_ptr(), rows, vocab,
+                                       logits.stride(0), _native.dtype_code(logits.dtype),
+                                       _native.ptr(ws), wsb, _native.stream_ptr(logits.device))
+    _native.check(rc, "argmax_rows")
+    return ids
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,vocab", [(128, 50257), (3, 100003), (40, 16385), (511, 20000),
+                                        (2, 40000)])
+def test_split_argmax_agrees_with_one_workgroup_per_row(dtype, rows, vocab):
+    print(f"[split argmax] {dtype} rows={rows} vocab={vocab}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows + vocab)
+    logits = (3 * torch.randn(rows, vocab + 5, generator=g, device=DEV)).to(dtype)[:, 2:2 + vocab]
+    # planted ties across slices, NaN in a late slice, +0 / -0, -inf rows
+    logits[0, 100] = logits[0, vocab - 3] = 50
+    logits[1, vocab // 2] = logits[1, vocab // 2 + 1] = 50
+    logits[-1, vocab - 1] = float("nan")
+    logits[-1, vocab // 3] = float("nan")
+    if rows > 3:
+        logits[2] = -1.0
+        logits[2, vocab - 1] = 0.0
+        logits[2, 7] = -0.0
+        logits[3] = float("-inf")
+    nb = _native.lib().pkv_argmax_workspace_bytes(rows, vocab, _native.dtype_code(dtype))
+    assert nb > 0
+    ws = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+    expect = logits.cpu().argmax(-1)
+    for rep in range(3):  # counters and key words are left at zero by every call
+        a = _abi_argmax(logits, ws)
+        b = _abi_argmax(logits, None)
+        torch.cuda.synchronize()
+        assert torch.equal(a.cpu(), expect), f"rep {rep}: split argmax differs from torch"
+        assert torch.equal(b.cpu(), expect), f"rep {rep}: one-workgroup argmax differs"
+    assert torch.equal(ws, torch.zeros_like(ws))
+
+
+def test_argmax_workspace_query():
+    L = _native.lib()
+    bf = _native.dtype_code(torch.bfloat16)
+    assert L.pkv_argmax_workspace_bytes(128, 50257, bf) == 128 * 256
+    assert L.pkv_argmax_workspace_bytes(512, 50257, bf) == 0  # one workgroup per row
+    assert L.pkv_argmax_workspace_bytes(128, 1000, bf) == 0   # one slice
+    assert L.pkv_argmax_workspace_bytes(4, 30000, bf) == 4 * 256

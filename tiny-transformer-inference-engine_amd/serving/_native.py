@@ -104,7 +104,9 @@ _SIGNATURES = {
     "pkv_linear_rope_qkv_rmsnorm": ([_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_float, _c_vp, _c_vp,
                                      _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _c_vp, _c_vp], _c_int),
-    "pkv_argmax_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp], _c_int),
+    "pkv_argmax_workspace_bytes": ([_c_i64, _c_i64, _c_int], _c_size),
+    "pkv_argmax_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _c_size, _c_vp],
+                        _c_int),
     "pkv_sample_rows": ([_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_float,
                          _c_vp, _c_int, _c_vp, _c_vp], _c_int),
     "pkv_stream_read": ([_c_vp, _c_i64, _c_vp, _c_int, _c_vp], _c_int),
@@ -189,28 +191,30 @@ def ptr(t) -> int | None:
 
 class Workspace:
     """Per-device scratch for split-K partials and the persistent kernel's
-    per-sequence records, grown on demand and reused (the library never
+    per-sequence records (slot "attention") and for the split-row argmax
+    kernel's counters and key words (slot "argmax"), one buffer per
+    (device, slot), grown on demand and reused (the library never
     allocates). Allocation goes through torch's caching allocator, so it is
     stream-ordered on the current stream; calls on other streams need their
     own Workspace."""
 
     def __init__(self):
-        self._bufs: dict[int, torch.Tensor] = {}
+        self._bufs: dict[tuple[int, str], torch.Tensor] = {}
 
-    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+    def get(self, device: torch.device, nbytes: int,
+            slot: str = "attention") -> torch.Tensor | None:
         if nbytes == 0:
             return None
         idx = device.index if device.index is not None else torch.cuda.current_device()
-        buf = self._bufs.get(idx)
+        buf = self._bufs.get((idx, slot))
         if buf is None or buf.numel() < nbytes:
             # grow geometrically so ragged batches do not reallocate every step
             size = max(nbytes, 0 if buf is None else 2 * buf.numel())
-            # zero-filled once: the persistent decode kernel's arrival
-            # counters (the first 256 KiB) must start at zero, and every
-            # call leaves them zero; the partials are written before they
-            # are read
+            # zero-filled once: the kernels' arrival counters (and the argmax
+            # key words) must start at zero, and every call leaves them zero;
+            # partials and records are written before they are read
             buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            self._bufs[idx] = buf
+            self._bufs[(idx, slot)] = buf
         return buf
 
 

@@ -343,11 +343,22 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
           or out.device != logits.device):
         raise ValueError("argmax_rows: out must be a contiguous int64 tensor of rows elements")
     stride = lg.stride(0) if rows > 1 else vocab
+    ws, wsb = _argmax_workspace(lg)
     rc = _native.lib().pkv_argmax_rows(out.data_ptr(), lg.data_ptr(), rows, vocab, stride,
-                                       _native.dtype_code(lg.dtype),
+                                       _native.dtype_code(lg.dtype), _native.ptr(ws), wsb,
                                        _native.stream_ptr(logits.device))
     _native.check(rc, "argmax_rows")
     return out
+
+
+def _argmax_workspace(lg):
+    """The split-row argmax's counters and key words: the "argmax" slot of
+    the current workspace (a graph step's own workspace under its scope)."""
+    rows, vocab = lg.shape
+    wsb = int(_native.lib().pkv_argmax_workspace_bytes(rows, vocab, _native.dtype_code(lg.dtype)))
+    if wsb == 0:
+        return None, 0
+    return _native.current_workspace().get(lg.device, wsb, slot="argmax"), wsb
 
 
 def sample_rows(logits: torch.Tensor, temperature: float, top_k: int, top_p: float,
