@@ -159,7 +159,7 @@ def _counters():
     per-sequence ones (the last int of each 16-byte record after them, and
     the one before it, which the wavefront-specialised kernel uses for its
     second head group)."""
-    buf = _native.WORKSPACE._bufs[torch.cuda.current_device()]
+    buf = _native.WORKSPACE._bufs[(torch.cuda.current_device(), "attention")]
     recs = buf[8 * 1024: 256 * 1024].view(torch.int32).view(-1, 4)
     return torch.cat([buf[: 8 * 1024].view(torch.int32), recs[:, 3], recs[:, 2]])
 

@@ -367,6 +367,32 @@ AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
     p.kind = -1;  // unsupported: reported by launch_attention
     return p;
   }
+  if (!mfma && max_blk >= 1 && decode_small_supported(dtype, max_q_len, group, d)) {
+    // small groups: one workgroup per (sequence, kv head, partition) of at
+    // least 256 tokens, longer bounds longer partitions so the longest
+    // context splits into at most 8 partials, merged in the same launch
+    p.kind = 4;
+    p.rows = group;
+    p.tiles_max = 1;
+    int plen = part_tokens > 0 ? part_tokens : 256;
+    if (part_tokens <= 0)
+      while (plen < 8192 && (int64_t)plen * 8 < kv_bound) plen *= 2;
+    plen = (plen + kChunk - 1) / kChunk * kChunk;
+    p.part_tokens = plen;
+    p.parts_max = ceil_div_h(kv_bound > 0 ? kv_bound : 1, plen);
+    if (p.parts_max < 1) p.parts_max = 1;
+    // split sequences are merged in the kernel: every (sequence, kv head)
+    // pair needs a counter of the workspace header
+    if (p.parts_max > 1 && virt > kMergeCtrMax) {
+      p.parts_max = 1;
+      p.part_tokens = (int)((kv_bound + kChunk - 1) / kChunk * kChunk);
+    }
+    p.ws_bytes = p.parts_max > 1
+                     ? kWsCounterBytes + (size_t)virt * p.parts_max * group * ((size_t)d + 2) *
+                                             sizeof(float)
+                     : 0;
+    return p;
+  }
   p.kind = mfma ? 1 : 0;
   p.rows = mfma ? group : kGenRows;
   p.tiles_max = ceil_div_h((int64_t)max_q_len * group, p.rows);
@@ -473,6 +499,13 @@ int launch_attention(const AttnArgs& a, const AttnPlan& p, int dtype,
     return launch_mfma<f16>(a, p, dtype, stream);
   }
   if (p.kind == 3) return launch_prefill_mfma(a, dtype, stream);
+  if (p.kind == 4) {
+    AttnArgs as = a;
+    if (p.parts_max > 1 && a.ws_o)
+      as.merge_ctr = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws_o) - kWsCounterBytes) +
+                     kMergeCtrOff;
+    return launch_decode_small(as, p, dtype, stream);
+  }
   switch (dtype) {
     case PKV_DTYPE_F32: return launch_generic<float>(a, p, stream);
     case PKV_DTYPE_F16: return launch_generic<f16>(a, p, stream);

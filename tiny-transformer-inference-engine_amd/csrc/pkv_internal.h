@@ -209,7 +209,8 @@ inline size_t sk_workspace_bytes(int group, int d) {
 
 struct AttnPlan {
   int kind;        // 0 = generic rows kernel, 1 = MFMA partition kernel,
-                   // 2 = MFMA persistent kernel, 3 = MFMA prefill kernel
+                   // 2 = MFMA persistent kernel, 3 = MFMA prefill kernel,
+                   // 4 = small-group decode kernel (decode_small.hip)
   bool ws;         // kind 2: the wavefront-specialised form where it applies
   int rows;        // rows per tile of the chosen kernel
   int part_tokens;
@@ -250,6 +251,32 @@ __device__ __forceinline__ int fetch_add_agent(int* p, int x) {
   global_i32* g = (global_i32*)p;
   asm volatile("" : "+v"(g));
   return __hip_atomic_fetch_add(g, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The value of lane (lane ^ S) of the wavefront, by VALU data movement:
+// DPP quad permutations (S = 1, 2), DPP row shifts selected by the lane bit
+// (S = 4, 8), and gfx950's cross-row swaps (S = 16, 32), instead of LDS
+// permutes.
+template <int S>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int x = __float_as_int(v);
+  const int lane = threadIdx.x & 63;
+  if constexpr (S == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  } else if constexpr (S == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  } else if constexpr (S == 4 || S == 8) {
+    const int up = __builtin_amdgcn_mov_dpp(x, 0x100 + S, 0xF, 0xF, true);  // row_shl: lane + S
+    const int dn = __builtin_amdgcn_mov_dpp(x, 0x110 + S, 0xF, 0xF, true);  // row_shr: lane - S
+    return __int_as_float((lane & S) ? dn : up);
+  } else if constexpr (S == 16) {
+    const auto a = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float(((lane >> 4) & 1) ? a[0] : a[1]);
+  } else {
+    static_assert(S == 32, "xor distance");
+    const auto a = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float((lane & 32) ? a[0] : a[1]);
+  }
 }
 
 // Counters of the split-K partition kernel's in-kernel merge, one per
@@ -293,6 +320,11 @@ __device__ __forceinline__ bool tile_geom(const AttnArgs& a, int s, int tile,
   return true;
 }
 
+
+// decode_small.hip: one query token per sequence, 1 / 2 / 4 / 8 query heads
+// per kv head, head dim 32 / 64 / 128, fp32 / bf16 / fp16 pools.
+bool decode_small_supported(int dtype, int max_q_len, int group, int d);
+int launch_decode_small(const AttnArgs& a, const AttnPlan& p, int dtype, hipStream_t stream);
 
 AttnPlan plan_attention(int n_seq, int max_q_len, int hq, int hkv, int d,
                         int max_blk, int block_size, int max_kv_len,

@@ -286,32 +286,6 @@ __device__ __forceinline__ uint64_t* smp_sort(uint64_t* ck, uint64_t* sk, int n)
   return ck;
 }
 
-// The value of lane (lane ^ S) of the wavefront, by VALU data movement:
-// DPP quad permutations (S = 1, 2), DPP row shifts selected by the lane bit
-// (S = 4, 8), and gfx950's cross-row swaps (S = 16, 32), instead of LDS
-// permutes.
-template <int S>
-__device__ __forceinline__ float lane_xor(float v) {
-  const int x = __float_as_int(v);
-  const int lane = threadIdx.x & 63;
-  if constexpr (S == 1) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
-  } else if constexpr (S == 2) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
-  } else if constexpr (S == 4 || S == 8) {
-    const int up = __builtin_amdgcn_mov_dpp(x, 0x100 + S, 0xF, 0xF, true);  // row_shl: lane + S
-    const int dn = __builtin_amdgcn_mov_dpp(x, 0x110 + S, 0xF, 0xF, true);  // row_shr: lane - S
-    return __int_as_float((lane & S) ? dn : up);
-  } else if constexpr (S == 16) {
-    const auto a = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
-    return __uint_as_float(((lane >> 4) & 1) ? a[0] : a[1]);
-  } else {
-    static_assert(S == 32, "xor distance");
-    const auto a = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
-    return __uint_as_float((lane & 32) ? a[0] : a[1]);
-  }
-}
-
 // Inclusive prefix sum across the wavefront's lanes: DPP row shifts within
 // each row of 16 lanes, then the totals of the earlier rows (read lanes).
 __device__ __forceinline__ float wave_incl_scan(float x) {
