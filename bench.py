@@ -415,9 +415,7 @@ def run_model(args, torch):
         logits = model.forward_step(ids, pool, meta)
         ids = fused_ops.argmax_rows(logits)
         # advance every sequence by one token, on the device
-        meta.positions.add_(1)
-        meta.start_pos.add_(1)
-        meta.seq_lens.add_(1)
+        meta.advance_()
 
     stream = torch.cuda.current_stream(dev)
     with torch.no_grad():

@@ -342,8 +342,8 @@ int pkv_silu_mul(void* out, const void* gate, const void* up, int64_t rows, int6
 /*
  * y = x W^T (+ bias) for few rows: x [m, k] (rows x_stride elements apart),
  * W [n, k] contiguous, bias [n] (nullable), y [m, n] contiguous; bf16 / fp16
- * storage, fp32 accumulation, one rounding. k must be a multiple of 32 and x
- * rows 16-byte aligned (PKV_ERR_UNSUPPORTED otherwise, as for fp32). Built
+ * / fp32 storage, fp32 accumulation, one rounding. k must be a multiple of
+ * 32 and x rows 16-byte aligned (PKV_ERR_UNSUPPORTED otherwise). Built
  * for decode steps (m up to a few hundred): the workgroups split k, so the
  * weight is streamed by the whole chip. The sum order is fixed: results are
  * deterministic and identical across the pkv_linear* entry points.

@@ -85,13 +85,13 @@ def test_workspace_sizing():
 def test_linear_validation_without_gpu():
     """Host-side rejections of the projection entry points (no launch)."""
     L = _native.lib()
-    # fp32 is not taken (the library GEMM serves it), k must be a multiple of 32
-    assert L.pkv_linear(16, 16, 16, None, 4, 8, 64, 64, 0, None) == -2
+    # an unknown dtype is not taken, k must be a multiple of 32
+    assert L.pkv_linear(16, 16, 16, None, 4, 8, 64, 64, 5, None) == -2
     assert L.pkv_linear(16, 16, 16, None, 4, 8, 40, 40, 2, None) == -2
     assert L.pkv_linear(None, 16, 16, None, 4, 8, 64, 64, 2, None) == -1
     assert L.pkv_linear(16, 16, 16, None, 4, 8, 64, 32, 2, None) == -1  # x_stride < k
     assert L.pkv_linear_swiglu(16, 16, 16, None, 4, 8, 48, 48, 1, None) == -2
-    assert L.pkv_linear_residual(16, 16, 16, None, 4, 8, 64, 64, 0, None) == -2
+    assert L.pkv_linear_residual(16, 16, 16, None, 4, 8, 64, 64, 5, None) == -2
     assert L.pkv_linear_residual(16, 16, 16, None, 4, 8, 64, 32, 2, None) == -1
     # the fused norm: k above 1024 refused before any launch, norm weight checked
     assert L.pkv_linear_swiglu_rmsnorm(16, 16, 16, 1e-5, 16, None, 4, 8, 1056, 1056, 2,

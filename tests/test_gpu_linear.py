@@ -1,7 +1,7 @@
 """The few-row projection kernels (csrc/linear.hip) through fused_ops.
 
-  pkv_linear           against the fp32 product of the same bf16 / fp16
-                       inputs: within one unit in the last place of the
+  pkv_linear           against the fp32 product of the same bf16 / fp16 /
+                       fp32 inputs: within one unit in the last place of the
                        storage type plus the fp32 summation-order slack
                        (4e-6 * sqrt(k) absolute for N(0, 1) inputs); rows
                        1 .. 256, features not a multiple of the 16-wide tile,
@@ -33,7 +33,7 @@ DEV = "cuda"
 
 
 def ulp(x: torch.Tensor) -> torch.Tensor:
-    mant = {torch.bfloat16: 7, torch.float16: 10}[x.dtype]
+    mant = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}[x.dtype]
     xf = x.float().abs().clamp_min(torch.finfo(x.dtype).tiny)
     return torch.exp2(torch.floor(torch.log2(xf)) - mant)
 
@@ -53,7 +53,7 @@ def check_linear(y, x, w, b):
     assert bool((err <= lim).all()), f"max err {float(err.max()):.3e}"
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,n,k,bias,strided", [
     (128, 1024, 1024, False, False),
     (128, 1152, 1024, True, False),
@@ -86,7 +86,7 @@ def test_linear_routes_unsupported_shapes_to_library_gemm():
     torch.testing.assert_close(fused_ops.linear(x, w), torch.nn.functional.linear(x, w))
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,h,k,bias", [(128, 1024, 1024, False), (7, 100, 64, True),
                                         (33, 2816, 1024, False)])
 def test_linear_swiglu_equals_linear_then_gate(dtype, m, h, k, bias):
@@ -110,7 +110,7 @@ def test_linear_swiglu_equals_linear_then_gate(dtype, m, h, k, bias):
                              f"two-step {expect[i, j].item()!r}")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,hq,hkv,d,k,bias", [(128, 16, 1, 64, 1024, False),
                                                (9, 32, 2, 128, 512, True),
                                                (40, 4, 1, 6, 64, False)])
@@ -162,7 +162,7 @@ def _first_diff(got, expect):
             f"two-step {expect[idx].item()!r}")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,n,k,bias,strided", [(128, 1024, 1024, False, False),
                                                 (1, 64, 32, True, False),
                                                 (17, 1000, 2816, False, True),
@@ -191,7 +191,7 @@ def _norm_inputs(dtype, m, k, seed, strided):
     return x, nw
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,h,k,bias,strided", [(128, 2816, 1024, False, False),
                                                 (1, 100, 32, True, False),
                                                 (7, 256, 96, False, True),
@@ -208,7 +208,7 @@ def test_linear_swiglu_rmsnorm_equals_norm_then_projection(dtype, m, h, k, bias,
     assert msg is None, msg
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,hq,hkv,d,k,bias,strided", [(128, 16, 1, 64, 1024, False, False),
                                                        (9, 4, 2, 128, 512, True, True),
                                                        (1, 8, 1, 64, 64, False, False)])

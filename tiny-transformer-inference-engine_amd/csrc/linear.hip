@@ -1,7 +1,8 @@
 // Projections of a decode step, y = x W^T (+ bias), for few rows (tokens):
-// bf16/fp16 storage, fp32 accumulation on MFMA 16x16x32, with the element-
-// wise op that follows the projection in a decoder block fused into the
-// epilogue:
+// bf16/fp16 storage with fp32 accumulation on MFMA 16x16x32, or fp32
+// storage on eight MFMA 16x16x4 fp32 steps per 32 k (the same lane layout),
+// with the element-wise op that follows the projection in a decoder block
+// fused into the epilogue:
 //   plain   y rounded to the storage type            (nn.Linear)
 //   swiglu  W = [gate rows; up rows]: out = g * sigmoid(g) * u of the rounded
 //           gate / up outputs, rounded once  (kernels/fused_swiglu/kernel.py:6-19)
@@ -324,13 +325,14 @@ int dispatch(const LinArgs& a, int dtype, hipStream_t stream) {
                 kLW * kKB * 32, a.k);
   if (dtype == PKV_DTYPE_BF16) return launch_t<bf16, EPI, NORM>(a, stream);
   if (dtype == PKV_DTYPE_F16) return launch_t<f16, EPI, NORM>(a, stream);
-  return fail(PKV_ERR_UNSUPPORTED, "linear: dtype %d (bf16 / fp16 only)", dtype);
+  if (dtype == PKV_DTYPE_F32) return launch_t<float, EPI, NORM>(a, stream);
+  return fail(PKV_ERR_UNSUPPORTED, "linear: dtype %d", dtype);
 }
 
 int check_common(const void* out, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
                  int64_t x_stride, int dtype) {
-  if (dtype != PKV_DTYPE_BF16 && dtype != PKV_DTYPE_F16)
-    return fail(PKV_ERR_UNSUPPORTED, "linear: dtype %d (bf16 / fp16 only)", dtype);
+  if (dtype != PKV_DTYPE_BF16 && dtype != PKV_DTYPE_F16 && dtype != PKV_DTYPE_F32)
+    return fail(PKV_ERR_UNSUPPORTED, "linear: dtype %d", dtype);
   if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x3fffffff || k > 0x7fffffff)
     return fail(PKV_ERR_INVALID, "linear: bad sizes m=%lld n=%lld k=%lld", (long long)m,
                 (long long)n, (long long)k);

@@ -67,6 +67,20 @@ struct Ops<f16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
+// fp32 operands (the few-row projections of fp32 models): the same lane
+// layout as the 16-bit forms (lane l: row l % 16 of A and column l % 16 of
+// B, 8 k-values of group l / 16), taken as eight v_mfma_f32_16x16x4_f32
+// steps, step j using element j of every lane (k-values j, 8 + j, 16 + j,
+// 24 + j of the 32), so each product is an fp32 sum over the same 32 k.
+template <>
+struct Ops<float> {
+  typedef float v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ floatx4 mma(v8 a, v8 b, floatx4 c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+    return c;
+  }
+};
 
 // fp8 pools: widening to bf16 / fp16 is exact; gfx950's
 // v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1 turns two fp8 bytes into two

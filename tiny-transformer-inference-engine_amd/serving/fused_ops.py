@@ -168,7 +168,8 @@ def _as_rows(x: torch.Tensor) -> torch.Tensor:
 
 
 def _linear_ok(x2: torch.Tensor, w: torch.Tensor, bias, n_features: int) -> bool:
-    return (x2.is_cuda and x2.dtype in (torch.bfloat16, torch.float16) and w.dtype == x2.dtype
+    return (x2.is_cuda and x2.dtype in (torch.bfloat16, torch.float16, torch.float32)
+            and w.dtype == x2.dtype
             and (bias is None or (bias.dtype == x2.dtype and bias.is_contiguous()))
             and 0 < x2.shape[0] <= LINEAR_MAX_ROWS and x2.shape[1] % 32 == 0
             and n_features <= LINEAR_MAX_FEATURES and w.is_contiguous()
@@ -181,8 +182,8 @@ def _x_stride(x2):
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None):
-    """x W^T + b. Few-row bf16/fp16 problems run on the split-K MFMA kernel
-    (pkv_linear); others on the library GEMM (F.linear)."""
+    """x W^T + b. Few-row bf16/fp16/fp32 problems run on the split-K MFMA
+    kernel (pkv_linear); others on the library GEMM (F.linear)."""
     x2 = _as_rows(x)
     n = weight.shape[0]
     if not _linear_ok(x2, weight, bias, n):

@@ -68,9 +68,7 @@ class DecodeStepGraph:
     def _step(self):
         logits = self.model.forward_step(self.ids, self.pool, self.meta)
         fused_ops.argmax_rows(logits, out=self.ids)
-        self.meta.positions.add_(1)
-        self.meta.start_pos.add_(1)
-        self.meta.seq_lens.add_(1)
+        self.meta.advance_()
         return logits
 
     def replay(self) -> torch.Tensor:

@@ -27,10 +27,28 @@ class PagedBatchMeta:
     max_q_len: int
     max_kv_len: int
     block_size: int
+    # seq_lens, start_pos and positions as one contiguous view (pack_batch_meta
+    # lays them out back to back), so a decode step advances them with one add
+    step_view: torch.Tensor | None = None
 
     @property
     def is_decode(self) -> bool:
         return self.max_q_len == 1 and self.num_tokens == self.num_seqs
+
+    def advance_(self) -> None:
+        """Every sequence one token further, on the device: seq_lens,
+        start_pos and positions + 1 (one kernel when they share step_view)."""
+        v = self.step_view
+        n, t = self.num_seqs, self.num_tokens
+        if (v is not None and v.numel() == 2 * n + t and v.dtype == torch.int32
+                and self.seq_lens.data_ptr() == v.data_ptr()
+                and self.start_pos.data_ptr() == v.data_ptr() + 4 * n
+                and self.positions.data_ptr() == v.data_ptr() + 8 * n):
+            v.add_(1)
+            return
+        self.positions.add_(1)
+        self.start_pos.add_(1)
+        self.seq_lens.add_(1)
 
 
 def _as_list(x):
@@ -85,7 +103,8 @@ def pack_batch_meta(block_tables, query_start_loc, positions, T: int, device,
                 raise AssertionError("slot mapping touches block 0, which is reserved")
 
     # one int32 host buffer -> one H2D copy; device views carved out of it
-    sizes = [n * max_blocks, n, n + 1, n, T]
+    # (seq_lens, start_pos, positions back to back: one add advances them)
+    sizes = [n * max_blocks, n + 1, n, n, T]
     buf = np.zeros(sum(sizes), dtype=np.int32)
     off = 0
     if max_blocks:
@@ -93,10 +112,10 @@ def pack_batch_meta(block_tables, query_start_loc, positions, T: int, device,
         for i, bt in enumerate(tables):
             tab[i, :len(bt)] = bt
     off += sizes[0]
-    buf[off:off + n] = seq_lens
-    off += n
     buf[off:off + n + 1] = qsl
     off += n + 1
+    buf[off:off + n] = seq_lens
+    off += n
     buf[off:off + n] = start_pos
     off += n
     buf[off:off + T] = pos
@@ -105,12 +124,14 @@ def pack_batch_meta(block_tables, query_start_loc, positions, T: int, device,
         host = host.pin_memory()
     dev = host.to(device, non_blocking=True)
     views = torch.split(dev, sizes)
+    step0 = sizes[0] + sizes[1]
     return PagedBatchMeta(
         block_tables=views[0].view(n, max_blocks),
-        seq_lens=views[1],
-        query_start_loc=views[2],
+        seq_lens=views[2],
+        query_start_loc=views[1],
         start_pos=views[3],
         positions=views[4],
+        step_view=dev[step0:step0 + 2 * n + T],
         num_seqs=n,
         num_tokens=T,
         max_blocks=max_blocks,
