@@ -8,7 +8,8 @@ a decode batch:
   - pools bit-identical afterwards (each new row written exactly once);
   - both MFMA decode kernels (partition: config-4 shape, persistent:
     config-5 shape with a long-context bound), block boundaries crossed;
-  - the fp32 generic kernel, where the library runs the two steps itself;
+  - the small-group kernel (fp32 config-2 shape; bf16 with sequences split
+    over several partitions and merged in the kernel; fp16 d 128);
   - a new row whose table entry is block 0 (reserved): skipped and flagged
     PKV_STATUS_BAD_BLOCK exactly like the stand-alone append.
 """
@@ -49,7 +50,9 @@ def copy_pool(pool):
     ("partition-cfg4", 128, 16, 64, torch.bfloat16, 256, 2048, 0),
     ("persistent-cfg5", 96, 32, 128, torch.bfloat16, 100, 3000, 8192),
     ("persistent-g16d128", 64, 16, 128, torch.float16, 1, 700, 4096),
-    ("generic-fp32", 24, 8, 32, torch.float32, 1, 300, 0),
+    ("small-fp32", 24, 8, 32, torch.float32, 1, 300, 0),
+    ("small-g4-bf16-split", 40, 4, 64, torch.bfloat16, 1, 3000, 0),
+    ("small-g2-fp16-d128", 16, 2, 128, torch.float16, 300, 900, 0),
 ])
 def test_fused_equals_two_calls(name, n, hq, d, dtype, lo, hi, bound):
     print(f"[fused append] {name}", flush=True)
@@ -69,8 +72,9 @@ def test_fused_equals_two_calls(name, n, hq, d, dtype, lo, hi, bound):
     assert torch.equal(lse_a, lse_b), f"{name}: lse differs"
 
 
-def test_fused_bad_block_is_skipped_and_flagged():
-    pool, meta, q, k, v = batch(8, 16, 64, torch.bfloat16, 40, 90, 16, 256, seed=22)
+@pytest.mark.parametrize("hq,d,dtype", [(16, 64, torch.bfloat16), (4, 32, torch.float32)])
+def test_fused_bad_block_is_skipped_and_flagged(hq, d, dtype):
+    pool, meta, q, k, v = batch(8, hq, d, dtype, 40, 90, 16, 256, seed=22)
     # the new row of sequence 3 falls into a table entry set to block 0
     s = 3
     pos = int(meta.start_pos[s].item())

@@ -242,9 +242,9 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
         v_new, block_tables, max_blk, query_start_loc, start_pos, n_seq, n_tokens, row_bytes,
         min_qlen, status, (hipStream_t)stream);
   };
-  // The split-K partition decode kernel and the MFMA prefill kernel (16-bit
-  // pools) take the append fused: the partition kernel the one row of each
-  // sequence, the prefill kernel every row of the batch (each workgroup a
+  // The split-K partition and small-group decode kernels and the MFMA
+  // prefill kernel (16-bit pools) take the append fused: the decode kernels
+  // the one row of each sequence, the prefill kernel every row of the batch (each workgroup a
   // share of the rows; its attention takes its own sequences' new rows from
   // k_new / v_new). For the persistent decode kernel the fused form measured
   // slower than a separate append launch (register pressure at 32 heads x
@@ -253,7 +253,7 @@ int attention_impl(void* out, float* lse, const void* q, const void* k_pool,
   if (!sp.mixed) {
     AttnArgs a = args_for(sp.dec, 0);
     if (k_new) {
-      if (sp.dec.kind == 1 || (sp.dec.kind == 3 && fuse_pre)) {
+      if (sp.dec.kind == 1 || sp.dec.kind == 4 || (sp.dec.kind == 3 && fuse_pre)) {
         a.k_new = k_new;
         a.v_new = v_new;
         a.new_pos = start_pos;

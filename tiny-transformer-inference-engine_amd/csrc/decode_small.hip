@@ -18,7 +18,9 @@
 // are combined by the same lane exchanges and the wavefronts through LDS.
 // A sequence split into several partitions is merged in the same launch
 // by the last partition to finish (arrival counter, as in the partition
-// decode kernel): no second launch.
+// decode kernel): no second launch. With the fused append (a.new_pos) the
+// step's new row is taken from k_new / v_new at its position and written
+// into the pool by the sequence's last partition.
 #include "pkv_internal.h"
 
 namespace pkv {
@@ -145,6 +147,10 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
   const int32_t* table = a.block_tables + (int64_t)s * a.max_blk;
   const int spec_blk0 = (part * a.part_tokens) >> a.bs_shift;
   const int tspec = table[max(0, min(spec_blk0 + tid, a.max_blk - 1))];
+  // fused append: the sequence's new row goes to position new_pos[s]; the
+  // partition holding that position takes it from k_new / v_new (the pool
+  // does not hold it yet) and the last partition writes it into the pool
+  const int npos = a.new_pos ? a.new_pos[s] : -1;
   uint4 qraw[G];
   if (s < a.n_tokens) {  // uniform
     const T* qp = static_cast<const T*>(a.q) + ((int64_t)s * a.hq + (int64_t)kvh * G) * D + piece * E;
@@ -185,6 +191,10 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
 
   const char* kbase = static_cast<const char*>(a.k_pool);
   const char* vbase = static_cast<const char*>(a.v_pool);
+  // the new row's pieces (query token q_begin of the sequence)
+  const int64_t new_off = (((int64_t)g.q_begin * a.hkv + kvh) * D + piece * E) * sizeof(T);
+  const char* knew = a.new_pos ? static_cast<const char*>(a.k_new) + new_off : nullptr;
+  const char* vnew = a.new_pos ? static_cast<const char*>(a.v_new) + new_off : nullptr;
   const int64_t row_bytes = (int64_t)a.hkv * D * sizeof(T);
   const int64_t piece_off = ((int64_t)kvh * D + piece * E) * sizeof(T);
   const int bmask = (1 << a.bs_shift) - 1;
@@ -217,8 +227,10 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
       bad |= !okb[j];
       const int64_t off =
           ((int64_t)(okb[j] ? blk : 0) * (bmask + 1) + (t & bmask)) * row_bytes + piece_off;
-      kr[j] = *reinterpret_cast<const uint4*>(kbase + off);
-      vr[j] = *reinterpret_cast<const uint4*>(vbase + off);
+      const bool isnew = t == npos;  // npos >= 0 only with the fused append
+      okb[j] = okb[j] || isnew;
+      kr[j] = *reinterpret_cast<const uint4*>(isnew ? knew : kbase + off);
+      vr[j] = *reinterpret_cast<const uint4*>(isnew ? vnew : vbase + off);
     }
 #pragma unroll
     for (int j = 0; j < kSmSteps; ++j) {
@@ -252,6 +264,31 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
   }
   }
   if (bad && a.status) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
+
+  // fused append: the last partition writes the new row into its pool slot,
+  // after the table and pool checks of the stand-alone append (status bits
+  // instead of the write); threads [0, LPT) the K pieces, [LPT, 2 LPT) V
+  if (a.new_pos && part == g.nparts - 1 && tid < 2 * LPT) {
+    const int page = npos >> a.bs_shift;
+    if (npos < 0 || page >= a.max_blk) {
+      if (a.status && tid == 0) atomicOr(a.status, PKV_STATUS_SHORT_TABLE);
+    } else {
+      const int64_t phys = table[page];
+      if (phys <= 0 || phys >= a.num_blocks) {
+        if (a.status && tid == 0) atomicOr(a.status, PKV_STATUS_BAD_BLOCK);
+      } else {
+        const bool is_v = tid >= LPT;
+        const int pc = tid % LPT;
+        const int64_t slot = (phys << a.bs_shift) + (npos & bmask);
+        const int64_t src = (((int64_t)g.q_begin * a.hkv + kvh) * D + pc * E) * sizeof(T);
+        const int64_t dst = ((slot * a.hkv + kvh) * D + pc * E) * sizeof(T);
+        const uint4 x = *reinterpret_cast<const uint4*>(
+            static_cast<const char*>(is_v ? a.v_new : a.k_new) + src);
+        *reinterpret_cast<uint4*>(static_cast<char*>(const_cast<void*>(is_v ? a.v_pool : a.k_pool)) +
+                                  dst) = x;
+      }
+    }
+  }
 
   // ---- combine: lane groups of the wavefront, then the wavefronts ----
   fold_wave<LPT, E, G>(st);
