@@ -174,6 +174,46 @@ def test_sample_errors_and_overflow_fallback():
         assert keep[tok[r]]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("vocab", [50257, 1000, 20])
+def test_sample_status_bits_16bit(dtype, vocab):
+    """Status bits and the -1 id of a declined row, per row, against the
+    per-element rule: NONFINITE for a non-finite logit, BAD_DISTRIBUTION for
+    a finite logit whose scaled value is not finite, SAMPLE_OVERFLOW for more
+    than 1024 values at the threshold."""
+    print(f"[sample status] {dtype} vocab={vocab}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(vocab)
+    base = (3 * torch.randn(6, vocab, generator=g, device=DEV)).to(dtype)
+    base[1, vocab // 2] = float("nan")
+    base[2, vocab - 1] = float("-inf")
+    base[3, 3] = float("inf")
+    base[4, 0] = float("nan")
+    base[4, 1] = 60000.0 if dtype == torch.float16 else 3e38
+    base[5] = 0.0
+    for temp in (1.0, 1e-3, 1e-36):
+        for r in range(6):
+            x = base[r:r + 1].contiguous()
+            xf = x.float().cpu().numpy()[0]
+            fin = np.isfinite(xf)
+            with np.errstate(over="ignore", invalid="ignore"):
+                y = xf.astype(np.float32) / np.float32(temp)
+            want = 0
+            if not fin.all():
+                want |= _native.PKV_STATUS_NONFINITE
+            if (fin & ~np.isfinite(y)).any():
+                want |= _native.PKV_STATUS_BAD_DISTRIBUTION
+            if want == 0 and r == 5 and vocab > 1024:
+                want = _native.PKV_STATUS_SAMPLE_OVERFLOW
+            u = torch.full((1,), 0.5, device=DEV)
+            ids, st = fused_ops.sample_rows(x, temp, 32, 0.9, u)
+            torch.cuda.synchronize()
+            assert int(st.item()) == want, f"row {r} temp {temp}: status {int(st.item())} want {want}"
+            if want:
+                assert int(ids.item()) == -1
+            else:
+                assert 0 <= int(ids.item()) < vocab
+
+
 # ---- split argmax rows (several workgroups per row, through the workspace)
 # against one workgroup per row (no workspace): the same ids
 
@@ -217,6 +257,55 @@ def test_split_argmax_agrees_with_one_workgroup_per_row(dtype, rows, vocab):
         assert torch.equal(a.cpu(), expect), f"rep {rep}: split argmax differs from torch"
         assert torch.equal(b.cpu(), expect), f"rep {rep}: one-workgroup argmax differs"
     assert torch.equal(ws, torch.zeros_like(ws))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_argmax_negative_nan_and_slice_ends(dtype):
+    """A NaN with its sign bit set is still the largest value; maxima in the
+    last 16-byte vector of a slice (the vector every clamped load of the
+    slice's last round re-reads) and in the scalar head and tail."""
+    rows, vocab = 64, 50257
+    print(f"[argmax slice ends] {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    base = (3 * torch.randn(rows, vocab + 8, generator=g, device=DEV)).to(dtype)
+    logits = base[:, 1:1 + vocab]  # rows start off the 16-byte grid
+    # NaN bit patterns with the sign bit set: 0xffc00001, 0xffc1, 0xfe01
+    ibits = {torch.float32: (torch.int32, -0x3fffff), torch.bfloat16: (torch.int16, -0x3f),
+             torch.float16: (torch.int16, -0x1ff)}[dtype]
+    nn = torch.tensor([ibits[1]], dtype=ibits[0]).view(dtype)[0].to(DEV)
+    assert bool(torch.isnan(nn)) and bool(torch.signbit(nn))
+    logits[0, 4000] = nn
+    logits[1, 4000] = nn
+    logits[1, 3000] = float("nan")
+    logits[2, 3000] = nn
+    logits[2, 4000] = float("nan")
+    es = logits.element_size()
+    V = 16 // es
+    nsplit = min(64, -(-vocab // (256 * 4 * V)))
+    for r in range(3, rows):
+        addr = logits[r].data_ptr()
+        head = min(vocab, ((16 - addr % 16) % 16) // es)
+        nvec = (vocab - head) // V
+        per = -(-nvec // nsplit)
+        k = r % (nsplit + 2)
+        if k == nsplit:
+            pos = max(head - 1, 0)            # the scalar head
+        elif k == nsplit + 1:
+            pos = vocab - 1                   # the scalar tail (or the last vector)
+        else:
+            pos = head + (min(nvec, (k + 1) * per) - 1) * V + (r % V)
+        logits[r, pos] = 60
+        if r % 2:
+            logits[r, (pos * 7) % vocab] = 60  # a tie elsewhere: the first wins
+    nb = _native.lib().pkv_argmax_workspace_bytes(rows, vocab, _native.dtype_code(dtype))
+    ws = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+    expect = logits.cpu().argmax(-1)
+    assert int(expect[0]) == 4000 and int(expect[1]) == 3000 and int(expect[2]) == 3000
+    a = _abi_argmax(logits, ws)
+    b = _abi_argmax(logits, None)
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), expect)
+    assert torch.equal(b.cpu(), expect)
 
 
 def test_argmax_workspace_query():

@@ -17,8 +17,11 @@
 //    count to P writes the index and puts both words back to zero for the
 //    next call. No workgroup waits for another.
 // Sampling uses one workgroup per row (a split form measured slower: the
-// slices' hand-over and merge cost more than the shorter passes saved).
+// slices' hand-over and merge cost more than the shorter passes saved);
+// 16-bit rows of up to 65536 entries are held in registers between its
+// steps (sample_rows_reg_kernel).
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 
 #include "pkv_internal.h"
@@ -45,79 +48,144 @@ constexpr int kKeyStride = kLineBytes / 8;
 // A workgroup streams its range of the row with 16-byte loads (a scalar head
 // up to the first 16-byte boundary, since rows of an odd vocabulary start
 // unaligned, then vectors, then a scalar tail), keeping per thread the
-// largest argmax key (argmax_key: the framework's order as one unsigned
+// largest argmax key (make_key: the framework's order as one unsigned
 // comparison); the keys are combined across the wavefront by lane swaps and
 // across wavefronts through LDS.
+//
+// 16-bit logits take a packed pass: per 32-bit word of two elements, the
+// two value keys with v_pk_* operations, each joined with the element's
+// position among the thread's elements of the round into a signed 32-bit
+// key (value key above, 31 - position below), and a 3-way maximum; once per
+// round the winner becomes a 64-bit key with its row index. About 4 VALU
+// instructions per element instead of 12. A round holding a NaN (its
+// magnitude bits above those of infinity) is redone with exact per-element
+// keys from the registers it was loaded into.
 
 constexpr int kAmThreads = 512;    // one workgroup per row
 constexpr int kAsThreads = 256;    // split rows
-constexpr int kAmUnroll = 4;      // 16-byte loads in flight per thread
+constexpr int kAmUnroll = 8;      // 16-byte loads in flight per thread
+constexpr int kNanKey = 0x7fffffff;
 
-// 64-bit key whose unsigned order is argmax order: the value's bits made
-// monotone (NaN above +inf, -0 as +0), then the complemented index (a lower
-// index is larger). 0 is below every key of an element.
-__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
-  unsigned hi;
-  if (v != v) {
-    hi = 0xffffffffu;
+// Value key: the two's complement of the sign-magnitude bits (so the order
+// is that of the numbers and -0, +0 share key 0); every NaN kNanKey, above
+// every number.
+template <typename T>
+__device__ __forceinline__ int value_key(T v) {
+  if constexpr (sizeof(T) == 2) {
+    unsigned short b;
+    __builtin_memcpy(&b, &v, 2);
+    constexpr unsigned kInf = std::is_same<T, bf16>::value ? 0x7f80u : 0x7c00u;
+    const unsigned m = b & 0x7fffu;
+    if (m > kInf) return kNanKey;
+    return (b & 0x8000u) ? -(int)m : (int)m;
   } else {
-    const unsigned u = v == 0.f ? 0u : __float_as_uint(v);
-    hi = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const unsigned u = __float_as_uint(v);
+    const unsigned m = u & 0x7fffffffu;
+    if (m > 0x7f800000u) return kNanKey;
+    return (u & 0x80000000u) ? -(int)m : (int)m;
   }
-  return ((uint64_t)hi << 32) | (uint64_t)(~(unsigned)i);
+}
+
+// 64-bit key whose unsigned order is argmax order: the value key (offset to
+// unsigned), then the complemented index (a lower index is larger). 0 is
+// below every key of an element.
+__device__ __forceinline__ uint64_t make_key(int vkey, int i) {
+  return ((uint64_t)((unsigned)vkey ^ 0x80000000u) << 32) | (uint64_t)(~(unsigned)i);
 }
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
 // The largest argmax key among vectors [v_lo, v_hi) of a row (16-byte
 // vectors after the scalar head of `head` elements), plus the head when
-// `with_head` and the scalar tail when `with_tail`, over NT threads: one
-// unsigned maximum per element, no branches. The loads of an iteration are
-// unconditional (indices past the range clamped onto its last vector, their
-// elements then skipped) so that all of them are in flight together: a load
-// under a branch gets a wait of its own.
+// `with_head` and the scalar tail when `with_tail`, over NT threads. The
+// loads of a round are unconditional (indices past the range clamped onto
+// its last vector) so that all of them are in flight together: a load under
+// a branch gets a wait of its own. A clamped copy of the last vector is
+// never the workgroup's winner: the thread that loads that vector at its
+// own position holds the same values at a lower index.
 template <typename T, int NT>
 __device__ __forceinline__ uint64_t argmax_scan(const T* __restrict__ row, int vocab, int head,
                                                 int v_lo, int v_hi, bool with_head,
                                                 bool with_tail, int tid) {
   constexpr int V = 16 / sizeof(T);
   uint64_t best = 0;
-  if (with_head && tid < head) best = argmax_key((float)row[tid], tid);
+  if (with_head && tid < head) best = make_key(value_key(row[tid]), tid);
   const T* vrow = row + head;
-  for (int v0 = v_lo + tid; v0 < v_hi; v0 += NT * kAmUnroll) {
+  for (int it0 = v_lo; it0 < v_hi; it0 += NT * kAmUnroll) {
+    const int v0 = it0 + tid;
     uint4 raw[kAmUnroll];
 #pragma unroll
     for (int u = 0; u < kAmUnroll; ++u)
       raw[u] = *reinterpret_cast<const uint4*>(vrow + (int64_t)min(v0 + u * NT, v_hi - 1) * V);
+    bool exact = true;
+    if constexpr (sizeof(T) == 2) {
+      constexpr unsigned kInf = std::is_same<T, bf16>::value ? 0x7f80u : 0x7c00u;
+      constexpr int kLast = kAmUnroll * V - 1;  // the round's last position (an inline constant)
+      int b32 = INT_MIN;
+      u16x2 mag = {0, 0};
 #pragma unroll
-    for (int u = 0; u < kAmUnroll; ++u) {
-      const int vv = v0 + u * NT;
-      T e[V];
-      __builtin_memcpy(e, &raw[u], 16);
+      for (int u = 0; u < kAmUnroll; ++u) {
+        const unsigned w4[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const uint64_t k = argmax_key((float)e[j], head + vv * V + j);
-        best = vv < v_hi ? max_u64(best, k) : best;
+        for (int w = 0; w < 4; ++w) {
+          const unsigned m = w4[w] & 0x7fff7fffu;
+          const s16x2 neg = __builtin_bit_cast(s16x2, w4[w]) >> (s16x2){15, 15};
+          const s16x2 key = (__builtin_bit_cast(s16x2, m) ^ neg) - neg;
+          mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, m));
+          const unsigned kp = __builtin_bit_cast(unsigned, key);
+          const int pos = u * V + 2 * w;  // position of element (u, 2w) in the round
+          const int klo = (int)((kp << 16) | (unsigned)(kLast - pos));
+          const int khi = (int)((kp & 0xffff0000u) | (unsigned)(kLast - 1 - pos));
+          b32 = max(b32, max(klo, khi));
+        }
+      }
+      exact = max((unsigned)mag.x, (unsigned)mag.y) > kInf;
+      if (!exact) {
+        const int pos = kLast - (b32 & 0xffff);
+        best = max_u64(best, make_key(b32 >> 16, head + (v0 + (pos / V) * NT) * V + pos % V));
+      }
+    }
+    if (exact) {
+#pragma unroll
+      for (int u = 0; u < kAmUnroll; ++u) {
+        const int vv = v0 + u * NT;
+        T e[V];
+        __builtin_memcpy(e, &raw[u], 16);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const uint64_t k = make_key(value_key(e[j]), head + vv * V + j);
+          best = vv < v_hi ? max_u64(best, k) : best;
+        }
       }
     }
   }
   if (with_tail) {
     const int nvec = (vocab - head) / V;
     for (int ix = head + nvec * V + tid; ix < vocab; ix += NT)
-      best = max_u64(best, argmax_key((float)row[ix], ix));
+      best = max_u64(best, make_key(value_key(row[ix]), ix));
   }
   return best;
+}
+
+template <int S>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
+  const unsigned lo = __float_as_uint(lane_xor<S>(__uint_as_float((unsigned)v)));
+  const unsigned hi = __float_as_uint(lane_xor<S>(__uint_as_float((unsigned)(v >> 32))));
+  return ((uint64_t)hi << 32) | lo;
 }
 
 // The workgroup's largest key; valid in thread 0.
 template <int NT>
 __device__ __forceinline__ uint64_t argmax_reduce(uint64_t best, int tid) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const unsigned lo = __shfl_xor((unsigned)(best & 0xffffffffu), o);
-    const unsigned hi = __shfl_xor((unsigned)(best >> 32), o);
-    best = max_u64(best, ((uint64_t)hi << 32) | lo);
-  }
+  best = max_u64(best, lane_xor64<1>(best));
+  best = max_u64(best, lane_xor64<2>(best));
+  best = max_u64(best, lane_xor64<4>(best));
+  best = max_u64(best, lane_xor64<8>(best));
+  best = max_u64(best, lane_xor64<16>(best));
+  best = max_u64(best, lane_xor64<32>(best));
   __shared__ uint64_t s_k[NT / 64];
   if ((tid & 63) == 0) s_k[tid >> 6] = best;
   __syncthreads();
@@ -236,6 +304,7 @@ __device__ __forceinline__ int smp_index(uint64_t k) { return (int)~(unsigned)(k
 // in its own blocks [128 (w + 4m), + 128), so those stages need no
 // workgroup barrier (a wavefront's LDS accesses complete in order), only
 // the stages with longer strides and the ones right after them.
+template <int NT>
 __device__ __forceinline__ void smp_bitonic(uint64_t* key, int n) {
   __syncthreads();
   int prev_stride = 0;
@@ -246,7 +315,7 @@ __device__ __forceinline__ void smp_bitonic(uint64_t* key, int n) {
       else
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       prev_stride = stride;
-      for (int p = threadIdx.x; p < (n >> 1); p += kSmpThreads) {
+      for (int p = threadIdx.x; p < (n >> 1); p += NT) {
         const int i = 2 * p - (p & (stride - 1));
         const int j = i + stride;
         const uint64_t ki = key[i], kj = key[j];
@@ -265,6 +334,7 @@ __device__ __forceinline__ void smp_bitonic(uint64_t* key, int n) {
 // its key by counting the larger ones (every lane reads the same entry at a
 // time: broadcast LDS reads, no branches) and writes it to sk[rank]; the
 // result is in sk. More: bitonic sort in place, result in ck.
+template <int NT>
 __device__ __forceinline__ uint64_t* smp_sort(uint64_t* ck, uint64_t* sk, int n) {
   const int tid = threadIdx.x;
   __syncthreads();
@@ -281,8 +351,8 @@ __device__ __forceinline__ uint64_t* smp_sort(uint64_t* ck, uint64_t* sk, int n)
   }
   int m = 64;
   while (m < n) m <<= 1;
-  for (int i = n + tid; i < m; i += kSmpThreads) ck[i] = 0;  // below every key
-  smp_bitonic(ck, m);
+  for (int i = n + tid; i < m; i += NT) ck[i] = 0;  // below every key
+  smp_bitonic<NT>(ck, m);
   return ck;
 }
 
@@ -552,7 +622,7 @@ __device__ __forceinline__ int smp_candidates(const T* __restrict__ row, SmpRang
   __syncthreads();
   nc = *L.cnt;
   if (nc > kSmpCand) return PKV_STATUS_SAMPLE_OVERFLOW;
-  sorted = smp_sort(L.ck, L.sk, nc);
+  sorted = smp_sort<kSmpThreads>(L.ck, L.sk, nc);
   return 0;
 }
 
@@ -655,6 +725,223 @@ __global__ __launch_bounds__(kSmpThreads) void sample_rows_kernel(
   smp_draw(sorted, L.qv, nc, k, top_p, uniforms[blockIdx.x], ids + blockIdx.x, tid);
 }
 
+// ------------------------------------------ sampling, rows held in registers
+//
+// 16-bit logits whose row fits one round of loads of a 512-thread workgroup
+// (R 16-byte vectors per thread): the row is read once and kept in
+// registers as value keys (value_key's order, computed two at a time with
+// v_pk_* operations in place of the loaded words), so step 3 reads no
+// memory. Same steps and results as sample_rows_kernel:
+//   1. per thread: the largest key and the largest magnitude (finiteness);
+//      the thread maximum of y is the value of that key divided by the
+//      temperature (division by a positive number is monotone);
+//   2. t0 = the k-th largest of the 512 thread maxima (wavefront 0 merges
+//      the eight sorted lists);
+//   3. kx = the smallest key whose scaled value is >= t0 (t0's own key at
+//      temperature 1, else a binary search over the keys); per vector the
+//      packed saturating differences key - kx are ANDed, and only vectors
+//      with a key >= kx are walked element by element and appended;
+//   4. the sort and the draw.
+// Clamped copies of the row's last vector (loads past the row) count for
+// neither the maxima nor the candidates.
+constexpr int kSrThreads = 512;
+
+// The 16-bit value of a key (the inverse of value_key for numbers).
+template <typename T>
+__device__ __forceinline__ float key16_value(int key) {
+  const unsigned short b =
+      key >= 0 ? (unsigned short)key : (unsigned short)(0x8000u | (unsigned)(-key));
+  T v;
+  __builtin_memcpy(&v, &b, 2);
+  return (float)v;
+}
+
+// The k-th largest (1 <= k <= 64) of the 512 thread values: each wavefront
+// sorts its 64 into wt, wavefront 0 merges the eight lists and leaves the
+// result in *out. Ends with a barrier.
+__device__ __forceinline__ void block_kth_largest512(float v, int k, float* wt, float* out) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  wt[tid] = wave_sort_desc(v);
+  __syncthreads();
+  if (tid < 64) {
+    const float a = wave_merge_top(wt[lane], wt[64 + lane]);
+    const float b = wave_merge_top(wt[128 + lane], wt[192 + lane]);
+    const float c = wave_merge_top(wt[256 + lane], wt[320 + lane]);
+    const float d = wave_merge_top(wt[384 + lane], wt[448 + lane]);
+    const float top = wave_merge_top(wave_merge_top(a, b), wave_merge_top(c, d));
+    // read with every lane active: inside a one-lane branch the compiler may
+    // leave lane k - 1's value of `top` uncomputed
+    const float kth = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(top), k - 1));
+    if (lane == 0) *out = kth;
+  }
+  __syncthreads();
+}
+
+template <typename T, int R>
+__global__ __launch_bounds__(kSrThreads) void sample_rows_reg_kernel(
+    int64_t* __restrict__ ids, const T* __restrict__ logits, int64_t row_stride, int vocab,
+    float temperature, int top_k, float top_p, const float* __restrict__ uniforms,
+    int* __restrict__ status) {
+  constexpr int V = 8;
+  constexpr int NT = kSrThreads;
+  constexpr unsigned kInf = std::is_same<T, bf16>::value ? 0x7f80u : 0x7c00u;
+  __shared__ uint64_t smp_ck[kSmpCand];
+  __shared__ uint64_t smp_sk[kSmpThreads];
+  __shared__ float smp_qv[kSmpCand];
+  __shared__ float smp_wt[kSrThreads];
+  __shared__ int smp_cnt, smp_flags;
+  __shared__ float smp_t0;
+  const int tid = threadIdx.x;
+  const T* row = logits + (int64_t)blockIdx.x * row_stride;
+  const int k = top_k < vocab ? top_k : vocab;
+  const bool unit = temperature == 1.f;
+  const int head = row_head(row, vocab, 2);
+  const int nvec = (vocab - head) / V;  // >= 1: the host sends rows of 16 elements or more
+  const int tail0 = head + nvec * V;
+  if (tid == 0) {
+    smp_cnt = 0;
+    smp_flags = 0;
+  }
+  uint4 kv[R];
+#pragma unroll
+  for (int u = 0; u < R; ++u)
+    kv[u] = *reinterpret_cast<const uint4*>(row + head + (int64_t)min(tid + u * NT, nvec - 1) * V);
+  // the thread's scalar element, if any: threads 0-7 the head, 8-15 the tail
+  const int xi = tid < head ? tid : (tid >= 8 && tid - 8 < vocab - tail0 ? tail0 + tid - 8 : -1);
+  int xk = INT_MIN;
+  unsigned xm = 0;
+  if (xi >= 0) {
+    unsigned short b;
+    __builtin_memcpy(&b, &row[xi], 2);
+    xm = b & 0x7fffu;
+    xk = (b & 0x8000u) ? -(int)xm : (int)xm;
+  }
+  // 1. keys in place, the thread's largest key and magnitude
+  s16x2 best = {-32768, -32768};
+  u16x2 mag = {0, 0};
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    unsigned w4[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
+    s16x2 vb = {-32768, -32768};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const unsigned m = w4[w] & 0x7fff7fffu;
+      const s16x2 neg = __builtin_bit_cast(s16x2, w4[w]) >> (s16x2){15, 15};
+      const s16x2 key = (__builtin_bit_cast(s16x2, m) ^ neg) - neg;
+      mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, m));
+      vb = __builtin_elementwise_max(vb, key);
+      w4[w] = __builtin_bit_cast(unsigned, key);
+    }
+    kv[u] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    if (tid + u * NT < nvec) best = __builtin_elementwise_max(best, vb);
+  }
+  const int tkey = max(max((int)best.x, (int)best.y), xk);
+  const unsigned tmag = max(max((unsigned)mag.x, (unsigned)mag.y), xm);
+  int flags = tmag >= kInf ? PKV_STATUS_NONFINITE : 0;
+  if (!unit) {
+    // a finite value whose scaled value is not finite: test the largest
+    // finite magnitude (with a non-finite value present, found element by
+    // element)
+    unsigned fm = tmag;
+    if (tmag >= kInf) {
+      fm = xm < kInf ? xm : 0;
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const unsigned w4[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int key = (int)(short)(w4[w] >> (16 * h));
+            const unsigned m = (unsigned)abs(key);
+            fm = m < kInf ? max(fm, m) : fm;
+          }
+      }
+    }
+    if (!isfinite(key16_value<T>((int)fm) / temperature)) flags |= PKV_STATUS_BAD_DISTRIBUTION;
+  }
+  float mx = -INFINITY;
+  if (tkey > -32768) {  // the thread holds an element
+    const float v = key16_value<T>(tkey);
+    mx = unit ? v : v / temperature;
+  }
+  // 2. t0 (the barriers inside also order the counters' set-up before use)
+  block_kth_largest512(mx, k, smp_wt, &smp_t0);
+  if (flags) atomicOr(&smp_flags, flags);
+  __syncthreads();
+  const int fl = smp_flags;
+  if (fl) {
+    if (tid == 0) {
+      ids[blockIdx.x] = -1;
+      if (status) atomicOr(status, fl);
+    }
+    return;
+  }
+  const float t0 = smp_t0;
+  // 3. the key threshold, then the candidates
+  int kx = -(int)kInf;
+  if (t0 > -INFINITY) {
+    if (unit) {
+      const T tv = (T)t0;
+      unsigned short b;
+      __builtin_memcpy(&b, &tv, 2);
+      kx = (b & 0x8000u) ? -(int)(b & 0x7fffu) : (int)(b & 0x7fffu);
+    } else {
+      // smallest key with key16_value(key) / temperature >= t0: the scaled
+      // value is monotone in the key, +inf's key qualifies, -inf's does not
+      int lo = -(int)kInf, hi = (int)kInf;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (key16_value<T>(mid) / temperature >= t0)
+          hi = mid;
+        else
+          lo = mid;
+      }
+      kx = hi;
+    }
+  }
+  const s16x2 kxv = {(short)kx, (short)kx};
+  auto append = [&](int key, int ix) {
+    const float v = key16_value<T>(key);
+    const float y = unit ? v : v / temperature;
+    const int at = atomicAdd(&smp_cnt, 1);
+    if (at < kSmpCand) smp_ck[at] = smp_pack(y, ix);
+  };
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    const unsigned w4[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
+    unsigned acc = 0xffffffffu;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      acc &= __builtin_bit_cast(unsigned,
+                                __builtin_elementwise_sub_sat(__builtin_bit_cast(s16x2, w4[w]), kxv));
+    const int vv = tid + u * NT;
+    if ((acc & 0x80008000u) != 0x80008000u && vv < nvec) {  // rare: a key >= kx
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int key = (int)(short)(w4[w] >> (16 * h));
+          if (key >= kx) append(key, head + vv * V + 2 * w + h);
+        }
+    }
+  }
+  if (xi >= 0 && xk >= kx) append(xk, xi);
+  __syncthreads();
+  const int nc = smp_cnt;
+  if (nc > kSmpCand) {
+    if (tid == 0) {
+      ids[blockIdx.x] = -1;
+      if (status) atomicOr(status, PKV_STATUS_SAMPLE_OVERFLOW);
+    }
+    return;
+  }
+  const uint64_t* sorted = smp_sort<kSrThreads>(smp_ck, smp_sk, nc);
+  if (tid >= 64) return;
+  smp_draw(sorted, smp_qv, nc, k, top_p, uniforms[blockIdx.x], ids + blockIdx.x, tid);
+}
+
 // ------------------------------------------------------------- host side
 
 // Workspace of the split argmax: [rows] arrival counters and [rows] key
@@ -748,6 +1035,22 @@ int pkv_sample_rows(int64_t* ids, const void* logits, int64_t rows, int64_t voca
     return fail(PKV_ERR_INVALID, "sample_rows: logits not aligned to the element size");
   if (rows == 0) return PKV_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t nvec_max = (vocab + 7) / 8;  // 16-byte vectors of a 16-bit row, at most
+  if (dtype != PKV_DTYPE_F32 && vocab >= 16 && nvec_max <= kSrThreads * 16) {
+    const dim3 grid((unsigned)rows), block(kSrThreads);
+    const bool r8 = nvec_max <= kSrThreads * 8;
+#define SR_LAUNCH(TT, RR)                                                                     \
+  hipLaunchKernelGGL((sample_rows_reg_kernel<TT, RR>), grid, block, 0, s, ids,                \
+                     static_cast<const TT*>(logits), row_stride, (int)vocab, temperature, top_k, \
+                     top_p, uniforms, status)
+    if (dtype == PKV_DTYPE_BF16) {
+      if (r8) SR_LAUNCH(bf16, 8); else SR_LAUNCH(bf16, 16);
+    } else {
+      if (r8) SR_LAUNCH(f16, 8); else SR_LAUNCH(f16, 16);
+    }
+#undef SR_LAUNCH
+    return check_launch("sample_rows_reg_kernel");
+  }
   const dim3 grid((unsigned)rows), block(kSmpThreads);
   if (dtype == PKV_DTYPE_BF16)
     hipLaunchKernelGGL((sample_rows_kernel<bf16>), grid, block, 0, s, ids,
