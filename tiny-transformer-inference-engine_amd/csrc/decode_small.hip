@@ -6,16 +6,21 @@
 // as pagedattn.forward (kernels/pagedattn/pagedattn.cu:142-447) for
 // q_len = 1.
 //
-// A workgroup of 4 wavefronts owns one (sequence, kv head, partition). A
+// A workgroup of 4 wavefronts owns one (sequence, kv head, partition) and
+// G of the group's query heads: a small batch splits each group's heads
+// over several workgroups (they read the same K / V rows, and no merge is
+// needed), so that the grid fills the CUs. A
 // token row (D elements) is split into 16-byte pieces, one per lane, so a
 // wavefront covers 64 / LPT tokens per step (LPT = lanes per row) and
-// every lane issues one 16-byte load for K and one for V per token, two
-// steps in flight. Each lane holds the G query heads' elements of its
+// every lane issues one 16-byte load for K and one for V per token, four
+// steps in flight (the 256 tokens of a planned partition in one round). Each lane holds the G query heads' elements of its
 // piece, pre-scaled by softmax_scale * log2(e); a token's partial dot
 // products are summed over its LPT lanes with DPP / cross-row swaps (VALU
 // data movement). Every lane group keeps an online softmax (max, sum, O
-// piece) per head over its tokens; at the end the groups of a wavefront
-// are combined by the same lane exchanges and the wavefronts through LDS.
+// piece) per head over its tokens; at the end every group's state goes to
+// LDS, each head's weights 2^(m - M) are formed once, and each output
+// column is one weighted sum over the groups (a fold through lane
+// exchanges, 4 levels of 8 heads x 10 values at bf16 d 32, took 3.5 us).
 // A sequence split into several partitions is merged in the same launch
 // by the last partition to finish (arrival counter, as in the partition
 // decode kernel): no second launch. With the fused append (a.new_pos) the
@@ -28,16 +33,22 @@ namespace {
 
 constexpr int kSmThreads = 256;
 constexpr int kSmWaves = kSmThreads / 64;
-constexpr int kSmSteps = 2;        // wavefront steps (tokens per lane group) in flight
 constexpr int kSmTblCap = 1024;    // table entries of a partition staged in LDS
+constexpr int64_t kSmallGridTarget = 256;  // workgroups a launch aims for (one per CU)
 constexpr float kSmLn2 = 0.69314718055994530942f;
 
-template <typename T, int D>
+template <typename T, int D, int G>
 struct SmallGeo {
   static constexpr int E = 16 / (int)sizeof(T);  // elements per 16-byte piece
   static constexpr int LPT = D / E;              // lanes per token row
   static constexpr int TPW = 64 / LPT;           // tokens per wavefront step
   static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "row pieces");
+  // wavefront steps (tokens per lane group) in flight: a planned partition
+  // of 256 tokens in one round, within the register budget (fewer heads,
+  // fewer registers per token)
+  static constexpr int STEPS_WANT = 256 / (4 * TPW);
+  static constexpr int STEPS_CAP = G <= 2 ? 8 : 4;
+  static constexpr int STEPS = STEPS_WANT < 1 ? 1 : (STEPS_WANT > STEPS_CAP ? STEPS_CAP : STEPS_WANT);
 };
 
 template <typename T, int E>
@@ -87,29 +98,6 @@ __device__ __forceinline__ void combine(HeadState<E>& a, float bm, float bl, con
   a.m = M;
 }
 
-// Combines the lane groups of a wavefront: lanes holding the same piece of
-// different token groups (distances LPT, 2 LPT, ..., 32).
-template <int S, int E, int G>
-__device__ __forceinline__ void fold_groups(HeadState<E> (&st)[G]) {
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float bo[E];
-#pragma unroll
-    for (int i = 0; i < E; ++i) bo[i] = lane_xor<S>(st[h].o[i]);
-    combine(st[h], lane_xor<S>(st[h].m), lane_xor<S>(st[h].l), bo);
-  }
-}
-
-template <int LPT, int E, int G>
-__device__ __forceinline__ void fold_wave(HeadState<E> (&st)[G]) {
-  if constexpr (LPT <= 1) fold_groups<1, E, G>(st);
-  if constexpr (LPT <= 2) fold_groups<2, E, G>(st);
-  if constexpr (LPT <= 4) fold_groups<4, E, G>(st);
-  if constexpr (LPT <= 8) fold_groups<8, E, G>(st);
-  if constexpr (LPT <= 16) fold_groups<16, E, G>(st);
-  if constexpr (LPT <= 32) fold_groups<32, E, G>(st);
-}
-
 template <typename T, int E>
 __device__ __forceinline__ void store_piece(T* dst, const float (&x)[E], float s) {
   T v[E];
@@ -122,12 +110,20 @@ __device__ __forceinline__ void store_piece(T* dst, const float (&x)[E], float s
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
-  using Geo = SmallGeo<T, D>;
+  using Geo = SmallGeo<T, D, G>;
   constexpr int E = Geo::E, LPT = Geo::LPT, TPW = Geo::TPW;
+  constexpr int kSmSteps = Geo::STEPS;
   constexpr int WG_STEP = kSmWaves * TPW;  // tokens of one workgroup step
+  // the final combination: s_o holds column d of head h for lane group gi
+  // at (h D + d) OP + gi (OP = NG + pad, so that the pieces of one
+  // wavefront's stores fall on distinct banks)
+  constexpr int NG = kSmWaves * TPW;  // lane groups of the workgroup
+  constexpr int OP = NG + (TPW / E > 1 ? TPW / E : 1);
+  static_assert(NG <= 64 && G * 32 <= kSmThreads, "one lane pair per group, 32 lanes per head");
   __shared__ int tbl[kSmTblCap];
-  __shared__ float s_o[kSmWaves][G][D];
-  __shared__ float s_ml[kSmWaves][G][2];
+  __shared__ float s_o[G * D * OP];
+  __shared__ float s_m[G][NG], s_l[G][NG], s_w[G][NG];
+  __shared__ float s_M[G], s_L[G];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -136,8 +132,16 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
   const int piece = lane % LPT;
   const int tg = lane / LPT;
   const int part = blockIdx.y;
-  const int s = blockIdx.x / a.hkv;
-  const int kvh = blockIdx.x - s * a.hkv;
+  // blockIdx.x = hs * (n_seq * hkv) + (s * hkv + kvh): head slice hs of the
+  // group (G of its a.group heads); the slices of one (sequence, kv head)
+  // are n_seq * hkv apart, so they share an XCD (and its L2) whenever that
+  // count is a multiple of 8
+  const int nsv = a.n_seq * a.hkv;
+  const int hs = blockIdx.x / nsv;
+  const int sv = blockIdx.x - hs * nsv;
+  const int s = sv / a.hkv;
+  const int kvh = sv - s * a.hkv;
+  const int h0 = kvh * a.group + hs * G;  // the slice's first query head
 
   // Requested before the sequence's metadata arrives (one round trip
   // instead of three): the partition's first table entries at the planned
@@ -153,7 +157,7 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
   const int npos = a.new_pos ? a.new_pos[s] : -1;
   uint4 qraw[G];
   if (s < a.n_tokens) {  // uniform
-    const T* qp = static_cast<const T*>(a.q) + ((int64_t)s * a.hq + (int64_t)kvh * G) * D + piece * E;
+    const T* qp = static_cast<const T*>(a.q) + ((int64_t)s * a.hq + h0) * D + piece * E;
 #pragma unroll
     for (int h = 0; h < G; ++h) qraw[h] = *reinterpret_cast<const uint4*>(qp + (int64_t)h * D);
   }
@@ -162,7 +166,7 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
   if (part >= g.nparts) return;
   const int kv_lo = part * g.part_len;
   const int kv_hi = min(kv_lo + g.part_len, g.kv_limit);
-  const int64_t qrow0 = (int64_t)g.q_begin * a.hq + (int64_t)kvh * G;
+  const int64_t qrow0 = (int64_t)g.q_begin * a.hq + h0;
   if (g.q_begin != s) {  // uniform
     const T* qp = static_cast<const T*>(a.q) + qrow0 * D + piece * E;
 #pragma unroll
@@ -268,7 +272,7 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
   // fused append: the last partition writes the new row into its pool slot,
   // after the table and pool checks of the stand-alone append (status bits
   // instead of the write); threads [0, LPT) the K pieces, [LPT, 2 LPT) V
-  if (a.new_pos && part == g.nparts - 1 && tid < 2 * LPT) {
+  if (a.new_pos && part == g.nparts - 1 && hs == 0 && tid < 2 * LPT) {
     const int page = npos >> a.bs_shift;
     if (npos < 0 || page >= a.max_blk) {
       if (a.status && tid == 0) atomicOr(a.status, PKV_STATUS_SHORT_TABLE);
@@ -290,69 +294,89 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
     }
   }
 
-  // ---- combine: lane groups of the wavefront, then the wavefronts ----
-  fold_wave<LPT, E, G>(st);
-  if (tg == 0) {
+  // ---- combine: every lane group's state through LDS; per head the
+  // reference M (the groups' largest max) and each group's weight
+  // 2^(m - M) once (32 lanes per head, two groups per lane), then per pair
+  // of output columns one weighted sum over the groups, in group order ----
+  {
+    const int gi = w * TPW + tg;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
 #pragma unroll
-      for (int i = 0; i < E; ++i) s_o[w][h][piece * E + i] = st[h].o[i];
+      for (int i = 0; i < E; ++i) s_o[(h * D + piece * E + i) * OP + gi] = st[h].o[i];
       if (piece == 0) {
-        s_ml[w][h][0] = st[h].m;
-        s_ml[w][h][1] = st[h].l;
+        s_m[h][gi] = st[h].m;
+        s_l[h][gi] = st[h].l;
       }
     }
   }
   __syncthreads();
-  // thread (h, pc) of the first G * LPT threads owns head h's piece pc
+  if (tid < 32 * G) {
+    const int h = tid >> 5, j = tid & 31;
+    const bool ha = j < NG, hb = j + 32 < NG;
+    const float ma = ha ? s_m[h][j] : -INFINITY;
+    const float mb = hb ? s_m[h][j + 32] : -INFINITY;
+    float M = fmaxf(ma, mb);
+    M = fmaxf(M, lane_xor<1>(M));
+    M = fmaxf(M, lane_xor<2>(M));
+    M = fmaxf(M, lane_xor<4>(M));
+    M = fmaxf(M, lane_xor<8>(M));
+    M = fmaxf(M, lane_xor<16>(M));
+    const float ref = M == -INFINITY ? 0.f : M;  // no key seen: weights 0, not NaN
+    const float wa = fast_exp2(ma - ref), wb = fast_exp2(mb - ref);
+    if (ha) s_w[h][j] = wa;
+    if (hb) s_w[h][j + 32] = wb;
+    float L = (ha ? s_l[h][j] * wa : 0.f) + (hb ? s_l[h][j + 32] * wb : 0.f);
+    L += lane_xor<1>(L);
+    L += lane_xor<2>(L);
+    L += lane_xor<4>(L);
+    L += lane_xor<8>(L);
+    L += lane_xor<16>(L);
+    if (j == 0) {
+      s_M[h] = M;
+      s_L[h] = L;
+    }
+  }
+  __syncthreads();
+  T* out = static_cast<T*>(a.out);
+  const bool split = g.nparts > 1;
+  const int64_t unit = (int64_t)blockIdx.x * a.parts_max + part;
+  for (int pi = tid; pi < G * D / 2; pi += kSmThreads) {
+    const int h = pi / (D / 2);
+    const int d = 2 * (pi - h * (D / 2));
+    const float* o0 = s_o + (h * D + d) * OP;
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll 8
+    for (int gg = 0; gg < NG; ++gg) {
+      const float wg = s_w[h][gg];
+      acc0 = fmaf(o0[gg], wg, acc0);
+      acc1 = fmaf(o0[OP + gg], wg, acc1);
+    }
+    const float L = s_L[h];
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    if (!split) {
+      const T pr[2] = {(T)(acc0 * inv), (T)(acc1 * inv)};
+      __builtin_memcpy(out + (qrow0 + h) * D + d, pr, sizeof(pr));
+      if (d == 0 && a.lse) a.lse[qrow0 + h] = L > 0.f ? (s_M[h] + log2f(L)) * kSmLn2 : INFINITY;
+    } else {
+      // split-K partial: O / sum in fp32 and (max, sum), written through to
+      // memory for the partition that completes the sequence's count
+      const float2 pr = make_float2(acc0 * inv, acc1 * inv);
+      uint64_t b;
+      __builtin_memcpy(&b, &pr, 8);
+      st_agent64(a.ws_o + (unit * G + h) * D + d, b);
+      if (d == 0) {
+        const float2 ml = make_float2(s_M[h], L);
+        __builtin_memcpy(&b, &ml, 8);
+        st_agent64(a.ws_ml + (unit * G + h) * 2, b);
+      }
+    }
+  }
+  if (!split) return;
+  // thread (h, pc) of the first G * LPT threads merges head h's piece pc
   const bool owner = tid < G * LPT;
   const int oh = tid / LPT;
   const int opc = tid - oh * LPT;
-  HeadState<E> fin;
-  if (owner) {
-    fin.m = -INFINITY;
-    fin.l = 0.f;
-#pragma unroll
-    for (int i = 0; i < E; ++i) fin.o[i] = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < kSmWaves; ++ww) {
-      float bo[E];
-#pragma unroll
-      for (int i = 0; i < E; ++i) bo[i] = s_o[ww][oh][opc * E + i];
-      combine(fin, s_ml[ww][oh][0], s_ml[ww][oh][1], bo);
-    }
-  }
-  T* out = static_cast<T*>(a.out);
-  if (g.nparts == 1) {
-    if (owner) {
-      const float inv = fin.l > 0.f ? 1.f / fin.l : 0.f;
-      store_piece<T, E>(out + (qrow0 + oh) * D + opc * E, fin.o, inv);
-      if (opc == 0 && a.lse)
-        a.lse[qrow0 + oh] = fin.l > 0.f ? (fin.m + log2f(fin.l)) * kSmLn2 : INFINITY;
-    }
-    return;
-  }
-
-  // ---- split-K: partial (O / sum in fp32, and (max, sum)), written through
-  // to memory; the partition that completes the sequence's count merges ----
-  const int64_t unit = (int64_t)blockIdx.x * a.parts_max + part;
-  if (owner) {
-    const float inv = fin.l > 0.f ? 1.f / fin.l : 0.f;
-    float* po = a.ws_o + (unit * G + oh) * D + opc * E;
-#pragma unroll
-    for (int i = 0; i < E; i += 2) {
-      const float2 pr = make_float2(fin.o[i] * inv, fin.o[i + 1] * inv);
-      uint64_t b;
-      __builtin_memcpy(&b, &pr, 8);
-      st_agent64(po + i, b);
-    }
-    if (opc == 0) {
-      const float2 ml = make_float2(fin.m, fin.l);
-      uint64_t b;
-      __builtin_memcpy(&b, &ml, 8);
-      st_agent64(a.ws_ml + (unit * G + oh) * 2, b);
-    }
-  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
@@ -398,8 +422,8 @@ __global__ __launch_bounds__(kSmThreads) void decode_small_kernel(AttnArgs a) {
 }
 
 template <typename T, int D>
-int launch_small_d(const AttnArgs& a, dim3 grid, hipStream_t stream) {
-  switch (a.group) {
+int launch_small_d(const AttnArgs& a, int heads, dim3 grid, hipStream_t stream) {
+  switch (heads) {
     case 1: hipLaunchKernelGGL((decode_small_kernel<T, D, 1>), grid, dim3(kSmThreads), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((decode_small_kernel<T, D, 2>), grid, dim3(kSmThreads), 0, stream, a); break;
     case 4: hipLaunchKernelGGL((decode_small_kernel<T, D, 4>), grid, dim3(kSmThreads), 0, stream, a); break;
@@ -409,10 +433,10 @@ int launch_small_d(const AttnArgs& a, dim3 grid, hipStream_t stream) {
 }
 
 template <typename T>
-int launch_small_t(const AttnArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.d == 32) return launch_small_d<T, 32>(a, grid, stream);
-  if (a.d == 64) return launch_small_d<T, 64>(a, grid, stream);
-  return launch_small_d<T, 128>(a, grid, stream);
+int launch_small_t(const AttnArgs& a, int heads, dim3 grid, hipStream_t stream) {
+  if (a.d == 32) return launch_small_d<T, 32>(a, heads, grid, stream);
+  if (a.d == 64) return launch_small_d<T, 64>(a, heads, grid, stream);
+  return launch_small_d<T, 128>(a, heads, grid, stream);
 }
 
 }  // namespace
@@ -426,10 +450,21 @@ bool decode_small_supported(int dtype, int max_q_len, int group, int d) {
 int launch_decode_small(const AttnArgs& a, const AttnPlan& p, int dtype, hipStream_t stream) {
   if (p.parts_max > 1 && !a.merge_ctr)
     return fail(PKV_ERR_WORKSPACE, "decode_small: split partitions need the workspace counters");
-  const dim3 grid(a.n_seq * a.hkv, p.parts_max);
-  if (dtype == PKV_DTYPE_F32) return launch_small_t<float>(a, grid, stream);
-  if (dtype == PKV_DTYPE_BF16) return launch_small_t<bf16>(a, grid, stream);
-  return launch_small_t<f16>(a, grid, stream);
+  // a small batch splits each group's heads over several workgroups (each
+  // reads the same K / V rows and owns some heads: no merge), until the
+  // grid has about one workgroup per CU
+  const int64_t nsv = (int64_t)a.n_seq * a.hkv;
+  int hsplit = 1;
+  while (hsplit < a.group && nsv * p.parts_max * hsplit < kSmallGridTarget &&
+         (p.parts_max == 1 || nsv * hsplit * 2 <= kMergeCtrMax))
+    hsplit *= 2;
+  if (nsv * hsplit > 0x7fffffff)
+    return fail(PKV_ERR_UNSUPPORTED, "decode_small: grid too large");
+  const dim3 grid((unsigned)(nsv * hsplit), p.parts_max);
+  const int heads = a.group / hsplit;
+  if (dtype == PKV_DTYPE_F32) return launch_small_t<float>(a, heads, grid, stream);
+  if (dtype == PKV_DTYPE_BF16) return launch_small_t<bf16>(a, heads, grid, stream);
+  return launch_small_t<f16>(a, heads, grid, stream);
 }
 
 }  // namespace pkv
