@@ -27,7 +27,9 @@
 // x 16*MB rows and splits K over its 8 wavefronts (each a contiguous K
 // range, so one wavefront reads 64-byte-or-longer runs of each weight row);
 // the wavefronts' fp32 partials are summed through LDS in a fixed order, so
-// results are deterministic and the same in every epilogue. The m tiles of
+// results are deterministic and the same in every epilogue. 16-bit operands
+// are loaded in whole cache lines and staged through LDS (an MFMA fragment
+// is 16 rows x 64 bytes, so fragment-shaped loads request every line twice). The m tiles of
 // one feature tile are dispatched to one XCD (block ids congruent mod 8), so
 // their common weight rows are fetched from HBM once, into that XCD's L2.
 #include "mfma_decode_common.h"
@@ -84,8 +86,27 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   using v8 = typename Ops<T>::v8;
   constexpr int MT = 16 * MB;
   constexpr int NS = EPI == kEpiSwiglu ? 2 : 1;  // weight row sets (gate, up)
-  __shared__ float red[NS][kLW][MT][kPitch];
+  // 16-bit operands are loaded in whole 128-byte lines and staged through a
+  // per-wavefront LDS region (rows of 4 K steps = 256 bytes, the 16-byte
+  // chunks of row r at chunk ^ (r % 16)); an MFMA fragment load touches 16
+  // rows x 64 bytes, so loading fragments straight from memory costs twice
+  // the cache-line requests (each line in two instructions)
+  constexpr bool STAGE = sizeof(T) == 2;
+  constexpr int RWS = 16 * (NS + MB);             // staged rows: W of each set, then x
+  constexpr int WAVE_STAGE = RWS * 256;           // bytes per wavefront
+  constexpr int RED_BYTES = NS * MT * kPitch * 4;  // one wavefront's partial sums
+  static_assert(!STAGE || RED_BYTES <= WAVE_STAGE, "partials fit the staging region");
+  __shared__ float red_f[STAGE ? 1 : NS * kLW * MT * kPitch];
+  __shared__ __attribute__((aligned(16))) char stage[STAGE ? kLW * WAVE_STAGE : 16];
   __shared__ float rsum[NORM ? kLW : 1][MT];
+  // wavefront ww's partial sums (set s, row, column): in its staging region
+  // once its operands are in registers
+  auto red = [&](int s, int ww, int row, int col) -> float& {
+    if constexpr (STAGE)
+      return reinterpret_cast<float*>(stage + ww * WAVE_STAGE)[(s * MT + row) * kPitch + col];
+    else
+      return red_f[((s * kLW + ww) * MT + row) * kPitch + col];
+  };
 
   const int b = blockIdx.x;
   const int xcd = b & 7;
@@ -94,7 +115,10 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   const int nt = (r / a.m_tiles) * 8 + xcd;
   if (nt >= a.n_tiles) return;  // padding tile: the whole workgroup leaves
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // scalar: the K-step tests below are then scalar branches. Under a branch
+  // the compiler takes as divergent it may drop the jump and rely on the
+  // EXEC mask, which an MFMA instruction does not obey
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15;
   const int n0 = nt * kNT;
   const int m0 = mt * MT;
@@ -151,8 +175,58 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   };
   // clamp target: the range's last step (a wavefront without steps re-reads step 0)
   const int s_last = s0 < s1 ? s1 - 1 : 0;
+  // staged form: load instruction (set q, j) covers rows 4j .. 4j + 3 of
+  // row set q, lane -> row 4j + (lane >> 4), chunk lane & 15 = 16-byte piece
+  // (chunk & 3) of K step sb + (chunk >> 2) (clamped like the direct loads)
+  char* const wst = stage + w * WAVE_STAGE;
+  u32x4 gl[NS + MB][4];
+  auto gload = [&](int sb) {
+    const int r4 = lane >> 4, ch = lane & 15;
+    const int st = min(sb + (ch >> 2), s_last);
 #pragma unroll
-  for (int j = 0; j < kKB; ++j) load(min(s0 + j, s_last), av[j], bv[j]);
+    for (int q = 0; q < NS + MB; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + r4;
+        const T* src = q < NS ? static_cast<const T*>(a.w) +
+                                    (int64_t)(min(n0 + r, a.n - 1) + q * a.n) * a.k
+                              : static_cast<const T*>(a.x) +
+                                    (int64_t)min(m0 + 16 * (q - NS) + r, a.m - 1) * a.x_stride;
+        gl[q][j] = *reinterpret_cast<const u32x4*>(src + st * 32 + (ch & 3) * 8);
+      }
+  };
+  auto gstage = [&]() {
+    const int r4 = lane >> 4, ch = lane & 15;
+#pragma unroll
+    for (int q = 0; q < NS + MB; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + r4;
+        *reinterpret_cast<u32x4*>(wst + ((q * 16 + r) * 16 + (ch ^ r)) * 16) = gl[q][j];
+      }
+  };
+  // fragments: lane -> row lane & 15, chunk 4j + (lane >> 4) for K step j
+  auto gfrag = [&]() {
+#pragma unroll
+    for (int j = 0; j < kKB; ++j) {
+      const int c = (4 * j + (lane >> 4)) ^ l16;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        av[j][s] = *reinterpret_cast<const v8*>(wst + ((s * 16 + l16) * 16 + c) * 16);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        bv[j][mb] = *reinterpret_cast<const v8*>(wst + (((NS + mb) * 16 + l16) * 16 + c) * 16);
+    }
+  };
+  if constexpr (STAGE) {
+    static_assert(kKB == 4, "a staged row holds 4 K steps");
+    gload(s0);
+    gstage();
+    gfrag();
+  } else {
+#pragma unroll
+    for (int j = 0; j < kKB; ++j) load(min(s0 + j, s_last), av[j], bv[j]);
+  }
   if constexpr (NORM) {
     // the whole K range of this wavefront is in registers (the host keeps
     // k within kLW * kKB steps): the rows' sums of squares, then the
@@ -211,8 +285,14 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
       }
     }
     if (sb + kKB < s1) {
+      if constexpr (STAGE) {
+        gload(sb + kKB);
+        gstage();
+        gfrag();
+      } else {
 #pragma unroll
-      for (int j = 0; j < kKB; ++j) load(min(sb + kKB + j, s_last), av[j], bv[j]);
+        for (int j = 0; j < kKB; ++j) load(min(sb + kKB + j, s_last), av[j], bv[j]);
+      }
     }
   }
 
@@ -241,7 +321,7 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[s][w][16 * mb + l16][(lane >> 4) * 4 + i] = acc[s][mb][i];
+      for (int i = 0; i < 4; ++i) red(s, w, 16 * mb + l16, (lane >> 4) * 4 + i) = acc[s][mb][i];
   __syncthreads();
 
   if (!live) return;
@@ -253,7 +333,7 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
     for (int j = 0; j < 2; ++j) {
       float sum = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < kLW; ++ww) sum += red[s][ww][ml][2 * p + j];
+      for (int ww = 0; ww < kLW; ++ww) sum += red(s, ww, ml, 2 * p + j);
       v[s][j] = sum;
     }
   if (a.bias) {
