@@ -62,6 +62,7 @@ def check_linear(y, x, w, b):
     (256, 48, 4096, False, False),
     (5, 3, 1024, True, False),
     (200, 2048, 544, False, True),
+    (64, 4200, 64, True, False),   # two 16-feature tiles per workgroup, a partial last one
 ])
 def test_linear_vs_fp32_product(dtype, m, n, k, bias, strided):
     print(f"[linear] {dtype} m={m} n={n} k={k} bias={bias} strided={strided}", flush=True)
@@ -166,7 +167,8 @@ def _first_diff(got, expect):
 @pytest.mark.parametrize("m,n,k,bias,strided", [(128, 1024, 1024, False, False),
                                                 (1, 64, 32, True, False),
                                                 (17, 1000, 2816, False, True),
-                                                (256, 48, 96, True, False)])
+                                                (256, 48, 96, True, False),
+                                                (96, 3000, 64, True, False)])
 def test_linear_residual_equals_linear_then_add(dtype, m, n, k, bias, strided):
     print(f"[linear_residual] {dtype} m={m} n={n} k={k} bias={bias}", flush=True)
     base = rand((m, k + (64 if strided else 0)), dtype, 41)

@@ -80,12 +80,18 @@ __device__ __forceinline__ float rnd(float x) {
   return (float)(T)fp32_value(x);
 }
 
-template <typename T, int MB, int EPI, bool NORM>
+// WIDE: a workgroup owns two 16-feature tiles (row sets 0 and 1 are
+// features n0 .. n0 + 15 and n0 + 16 .. n0 + 31), for grids that would
+// otherwise take more than one workgroup per CU (each reads its x rows for
+// twice the features)
+template <typename T, int MB, int EPI, bool NORM, bool WIDE>
 __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
 #pragma clang fp contract(off)
   using v8 = typename Ops<T>::v8;
   constexpr int MT = 16 * MB;
-  constexpr int NS = EPI == kEpiSwiglu ? 2 : 1;  // weight row sets (gate, up)
+  static_assert(!(WIDE && EPI == kEpiSwiglu), "SwiGLU's row sets are gate and up");
+  constexpr int NS = EPI == kEpiSwiglu || WIDE ? 2 : 1;  // weight row sets
+  constexpr int FT = WIDE ? 2 * kNT : kNT;               // output features per tile
   // 16-bit operands are loaded in whole 128-byte lines and staged through a
   // per-wavefront LDS region (rows of 4 K steps = 256 bytes, the 16-byte
   // chunks of row r at chunk ^ (r % 16)); an MFMA fragment load touches 16
@@ -120,28 +126,38 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   // EXEC mask, which an MFMA instruction does not obey
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15;
-  const int n0 = nt * kNT;
+  const int n0 = nt * FT;
   const int m0 = mt * MT;
+  // weight row of set s for tile row r (clamped into range; the outputs of
+  // clamped rows are never stored): SwiGLU's up rows follow its n gate rows
+  auto wrow_of = [&](int s, int r) -> int64_t {
+    if constexpr (EPI == kEpiSwiglu)
+      return (int64_t)min(n0 + r, a.n - 1) + (int64_t)s * a.n;
+    else
+      return (int64_t)min(n0 + kNT * s + r, a.n - 1);
+  };
 
-  // operand rows (clamped into range; their outputs are never stored)
+  // operand rows
   const T* wrow[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s)
-    wrow[s] = static_cast<const T*>(a.w) +
-              (int64_t)(min(n0 + l16, a.n - 1) + s * a.n) * a.k + (lane >> 4) * 8;
+    wrow[s] = static_cast<const T*>(a.w) + wrow_of(s, l16) * a.k + (lane >> 4) * 8;
   const T* xrow[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
     xrow[mb] = static_cast<const T*>(a.x) + (int64_t)min(m0 + 16 * mb + l16, a.m - 1) * a.x_stride +
                (lane >> 4) * 8;
 
-  // epilogue mapping: one thread per (row, feature pair)
+  // epilogue mapping: one thread per (row, feature pair); pair p of a wide
+  // tile is pair p % 8 of row set p / 8
+  constexpr int PPR = FT / 2;  // feature pairs per row
+  static_assert(MT * PPR <= kLThreads, "one thread per pair");
   const int t = threadIdx.x;
-  const int ml = t >> 3;
-  const int p = t & 7;
+  const int ml = t / PPR;
+  const int p = t % PPR;
   const int m = m0 + ml;
   const int n = n0 + 2 * p;
-  const bool live = t < MT * (kNT / 2) && m < a.m && n < a.n;
+  const bool live = t < MT * PPR && m < a.m && n < a.n;
   // rope: the row's position is requested before the operands
   const int qn = a.hq * a.d;
   const int kn = a.hkv * a.d;
@@ -188,8 +204,7 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * j + r4;
-        const T* src = q < NS ? static_cast<const T*>(a.w) +
-                                    (int64_t)(min(n0 + r, a.n - 1) + q * a.n) * a.k
+        const T* src = q < NS ? static_cast<const T*>(a.w) + wrow_of(q, r) * a.k
                               : static_cast<const T*>(a.x) +
                                     (int64_t)min(m0 + 16 * (q - NS) + r, a.m - 1) * a.x_stride;
         gl[q][j] = *reinterpret_cast<const u32x4*>(src + st * 32 + (ch & 3) * 8);
@@ -326,20 +341,23 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
 
   if (!live) return;
   const bool two = n + 1 < a.n;
-  float v[NS][2];
+  constexpr int NV = EPI == kEpiSwiglu ? 2 : 1;  // value sets per thread (gate, up)
+  const int se = WIDE ? p / (kNT / 2) : 0;      // the row set of a wide tile's pair
+  const int pc = WIDE ? p % (kNT / 2) : p;
+  float v[NV][2];
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
+  for (int s = 0; s < NV; ++s)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       float sum = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < kLW; ++ww) sum += red(s, ww, ml, 2 * p + j);
+      for (int ww = 0; ww < kLW; ++ww) sum += red(WIDE ? se : s, ww, ml, 2 * pc + j);
       v[s][j] = sum;
     }
   if (a.bias) {
     const T* bias = static_cast<const T*>(a.bias);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NV; ++s) {
       v[s][0] = fp32_value(v[s][0] + (float)bias[s * a.n + n]);
       if (two) v[s][1] = fp32_value(v[s][1] + (float)bias[s * a.n + n + 1]);
     }
@@ -382,20 +400,32 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   }
 }
 
-template <typename T, int EPI, bool NORM>
-int launch_t(LinArgs a, hipStream_t stream) {
-  const int mb = a.m <= 16 ? 1 : 2;
+template <typename T, int EPI, bool NORM, bool WIDE>
+int launch_w(LinArgs a, int mb, hipStream_t stream) {
+  constexpr int FT = WIDE ? 2 * kNT : kNT;
   a.m_tiles = (a.m + 16 * mb - 1) / (16 * mb);
-  a.n_tiles = (a.n + kNT - 1) / kNT;
+  a.n_tiles = (a.n + FT - 1) / FT;
   const int64_t blocks = (int64_t)((a.n_tiles + 7) / 8) * 8 * a.m_tiles;
   if (blocks > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "linear: %lld tiles", (long long)blocks);
   if (mb == 1)
-    hipLaunchKernelGGL((linear_kernel<T, 1, EPI, NORM>), dim3((unsigned)blocks), dim3(kLThreads),
-                       0, stream, a);
+    hipLaunchKernelGGL((linear_kernel<T, 1, EPI, NORM, WIDE>), dim3((unsigned)blocks),
+                       dim3(kLThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((linear_kernel<T, 2, EPI, NORM>), dim3((unsigned)blocks), dim3(kLThreads),
-                       0, stream, a);
+    hipLaunchKernelGGL((linear_kernel<T, 2, EPI, NORM, WIDE>), dim3((unsigned)blocks),
+                       dim3(kLThreads), 0, stream, a);
   return check_launch("linear_kernel");
+}
+
+template <typename T, int EPI, bool NORM>
+int launch_t(LinArgs a, hipStream_t stream) {
+  const int mb = a.m <= 16 ? 1 : 2;
+  // 16-bit operands (staged through LDS: one workgroup per CU): a grid of
+  // more 16-feature tiles than CUs takes two tiles per workgroup instead
+  if constexpr (sizeof(T) == 2 && EPI != kEpiSwiglu) {
+    const int64_t tiles = (int64_t)((a.m + 16 * mb - 1) / (16 * mb)) * ((a.n + kNT - 1) / kNT);
+    if (tiles > device_cu_count()) return launch_w<T, EPI, NORM, true>(a, mb, stream);
+  }
+  return launch_w<T, EPI, NORM, false>(a, mb, stream);
 }
 
 template <int EPI, bool NORM = false>
