@@ -166,6 +166,28 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
   if constexpr (EPI == kEpiRope) {
     if (rot) pos = a.positions[m];
   }
+  // residual: the stream's two values and the bias are requested before the
+  // operands too (the epilogue would otherwise wait for them after the
+  // partial sums); each (row, feature) is read and written by this thread only
+  const bool two_e = n + 1 < a.n;
+  float res[2] = {0.f, 0.f};
+  if constexpr (EPI == kEpiResid) {
+    if (live) {
+      const T* o = static_cast<const T*>(a.out) + (int64_t)m * a.n + n;
+      res[0] = (float)o[0];
+      if (two_e) res[1] = (float)o[1];
+    }
+  }
+  constexpr int NVB = EPI == kEpiSwiglu ? 2 : 1;  // bias sets (gate, up)
+  float bia[NVB][2] = {};
+  if (a.bias && live) {
+    const T* bias = static_cast<const T*>(a.bias);
+#pragma unroll
+    for (int s = 0; s < NVB; ++s) {
+      bia[s][0] = (float)bias[s * a.n + n];
+      if (two_e) bia[s][1] = (float)bias[s * a.n + n + 1];
+    }
+  }
 
   // this wavefront's contiguous range of 32-wide K steps
   const int ksteps = a.k >> 5;
@@ -355,11 +377,10 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
       v[s][j] = sum;
     }
   if (a.bias) {
-    const T* bias = static_cast<const T*>(a.bias);
 #pragma unroll
     for (int s = 0; s < NV; ++s) {
-      v[s][0] = fp32_value(v[s][0] + (float)bias[s * a.n + n]);
-      if (two) v[s][1] = fp32_value(v[s][1] + (float)bias[s * a.n + n + 1]);
+      v[s][0] = fp32_value(v[s][0] + bia[s][0]);
+      if (two) v[s][1] = fp32_value(v[s][1] + bia[s][1]);
     }
   }
 
@@ -369,8 +390,8 @@ __global__ __launch_bounds__(kLThreads) void linear_kernel(LinArgs a) {
     if (two) o[1] = (T)v[0][1];
   } else if constexpr (EPI == kEpiResid) {
     T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
-    o[0] = (T)fp32_value((float)o[0] + rnd<T>(v[0][0]));
-    if (two) o[1] = (T)fp32_value((float)o[1] + rnd<T>(v[0][1]));
+    o[0] = (T)fp32_value(res[0] + rnd<T>(v[0][0]));
+    if (two) o[1] = (T)fp32_value(res[1] + rnd<T>(v[0][1]));
   } else if constexpr (EPI == kEpiSwiglu) {
     T* o = static_cast<T*>(a.out) + (int64_t)m * a.n + n;
 #pragma unroll
