@@ -63,6 +63,8 @@ def check_linear(y, x, w, b):
     (5, 3, 1024, True, False),
     (200, 2048, 544, False, True),
     (64, 4200, 64, True, False),   # two 16-feature tiles per workgroup, a partial last one
+    (16, 64, 256, False, False),   # one K step per wavefront: the skipped steps add nothing
+    (9, 48, 768, True, False),     # three K steps per wavefront
 ])
 def test_linear_vs_fp32_product(dtype, m, n, k, bias, strided):
     print(f"[linear] {dtype} m={m} n={n} k={k} bias={bias} strided={strided}", flush=True)
