@@ -34,7 +34,7 @@ def check(logits):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("rows,vocab", [(128, 50257), (3, 1), (5, 7), (9, 8), (2, 100003),
-                                        (64, 4096)])
+                                        (64, 4096), (600, 3000), (520, 70001)])
 def test_argmax_random(dtype, rows, vocab):
     print(f"[argmax] {dtype} rows={rows} vocab={vocab}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(rows * 7 + vocab)
@@ -135,6 +135,35 @@ def test_sample_rows_ties_and_strided_rows():
     wide = torch.zeros(40, 3200, dtype=torch.bfloat16, device=DEV)
     wide[:, 100:3100] = logits
     _check_rows(wide[:, 100:3100], 1.0, 16, 0.77, seed=6, min_checked=0.6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("vocab", [50257, 65536, 65537, 1000])
+def test_sample_top_k_1_picks_head_and_tail_maxima(dtype, vocab):
+    """top_k 1 is the argmax (a single maximum) also when the maximum sits
+    in a row's scalar head (before the first 16-byte boundary) or its scalar
+    tail, on rows that start off the 16-byte grid; 65536 entries is the
+    largest row held in registers, 65537 the smallest one that is not."""
+    rows = 24
+    print(f"[sample head/tail] {dtype} vocab={vocab}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(vocab)
+    base = torch.randn(rows, vocab + 8, generator=g, device=DEV).to(dtype)
+    x = base[:, 3:3 + vocab]
+    es = x.element_size()
+    for r in range(rows):
+        head = min(vocab, ((16 - x[r].data_ptr() % 16) % 16) // es)
+        tail = (vocab - head) % (16 // es)
+        if r % 3 == 0 and head > 0:
+            x[r, r % head] = 9.0
+        elif r % 3 == 1 and tail > 0:
+            x[r, vocab - 1 - r % tail] = 9.0
+        else:
+            x[r, (r * 977) % vocab] = 9.0  # (no tie: tied maxima all survive top_k 1)
+    u = torch.rand(rows, generator=g, device=DEV)
+    ids, st = fused_ops.sample_rows(x, 1.0, 1, 1.0, u)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    assert torch.equal(ids.cpu(), x.float().cpu().argmax(-1))
 
 
 def test_sample_top_k_1_is_argmax_and_distribution_matches():
